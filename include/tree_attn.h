@@ -1,0 +1,103 @@
+/*
+ * tree_attn.h -- C ABI of the MI355X (gfx950) tree-shared decode-attention backend.
+ *
+ * Replaces the Triton kernels of the reference's src/tree_attention/kernels.py:
+ *   _segment (kernels.py:8-55)   -> ta_segment
+ *   _merge   (kernels.py:58-83)  -> ta_merge
+ *   attention_matrix's launch sequence (kernels.py:152-168) -> ta_attention_matrix
+ *
+ * Conventions
+ *   - Every pointer is a device pointer owned by the caller; the library allocates
+ *     nothing, keeps no state between calls and never synchronises the host.
+ *   - Launches are asynchronous on `stream` (a hipStream_t; NULL = default stream).
+ *   - Return value: 0 on success, a HIP error code from the launch, or one of the
+ *     TA_ERR_* argument errors below.  ta_error_string() names any of them.
+ *   - dtype: TA_BF16 or TA_FP16, shared by q, kp, vp and out.  Accumulation, the
+ *     partial outputs and the log-sum-exp values are fp32.
+ *   - Layouts (row-major, contiguous, base 16-byte aligned):
+ *       q     [nreq, hq, d]        query of each request (kernels.py:157 permutes it;
+ *                                  here the kernel indexes it directly)
+ *       kp    [hk, d, tcap]        K pool, token-minor (kernels.py:144, qwen.py:27)
+ *       vp    [hk, tcap, d]        V pool                 (kernels.py:145, qwen.py:28)
+ *       part  [nslot, hq, d] fp32  normalised partial output per (job, request)
+ *       lse   [nslot, hq]    fp32  natural-log log-sum-exp of the same rows
+ *       out   [nreq, hq, d]
+ *   - Job j covers physical tokens [kstart[j], kstart[j] + klen[j]) for the requests
+ *     qids[j*maxr + 0 .. qlen[j]-1]; its partial rows are slots rowbase[j] + i.
+ *     klen[j] == 0 yields a zero partial with lse = -inf, which the merge ignores.
+ *   - Supported: d in {32, 64, 128}, hq % hk == 0.
+ */
+#ifndef TREE_ATTN_H
+#define TREE_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TA_BF16 0
+#define TA_FP16 1
+
+/* segment work-item kinds */
+#define TA_SMALL 0      /* jobs with <= 16 query rows; items = job ids, grid (n, hk)        */
+#define TA_LARGE64 1    /* row tiles of 64 rows;  items = (job, first row, kv head) triples */
+#define TA_LARGE128 2   /* row tiles of 128 rows; items = (job, first row, kv head) triples */
+#define TA_LARGE256 3   /* row tiles of 256 rows; items = (job, first row, kv head) triples */
+
+#define TA_ERR_ARG 1001      /* null pointer, bad size or unsupported shape */
+#define TA_ERR_ALIGN 1002    /* q / kp / vp / part / out not 16-byte aligned */
+#define TA_ERR_DTYPE 1003    /* dtype not TA_BF16 / TA_FP16 */
+
+/* Everything one attention_matrix call needs besides q, kp, vp and out.
+ * Built once per plan by the host (kernels.py:103-141 `prepare`). */
+typedef struct ta_plan {
+    const int32_t *qids;      /* [njobs * maxr]                                   */
+    const int32_t *kstart;    /* [njobs] first physical token of each job          */
+    const int32_t *qlen;      /* [njobs] requests per job                          */
+    const int32_t *klen;      /* [njobs] tokens per job (device-updatable)         */
+    const int32_t *rowbase;   /* [njobs] first partial slot of each job            */
+    const int32_t *slots;     /* [nreq * maxs] partial slots of each request       */
+    const int32_t *counts;    /* [nreq] number of slots of each request            */
+    const int32_t *items[4];  /* work items per kind TA_SMALL .. TA_LARGE256       */
+    int32_t n_items[4];
+    float *part;
+    float *lse;
+    int32_t njobs, maxr, maxs, nreq, nslot;
+    int32_t hq, hk, d, dtype;
+} ta_plan;
+
+/* Version string of the library build. */
+const char *ta_version(void);
+
+/* Human-readable name of a return code of this library. */
+const char *ta_error_string(int code);
+
+/* Grouped partial attention of physical KV segments (replaces _segment,
+ * kernels.py:8-55, and its launch at kernels.py:158-165).  Writes the
+ * normalised partial output and the log-sum-exp of every (job, request, head)
+ * row of the given work items. */
+int ta_segment(const void *q, const void *kp, const void *vp,
+               const int32_t *qids, const int32_t *kstart, const int32_t *qlen,
+               const int32_t *klen, const int32_t *rowbase,
+               const int32_t *items, int32_t n_items, int32_t kind,
+               float *part, float *lse,
+               int32_t nreq, int32_t hq, int32_t hk, int32_t d, int32_t tcap,
+               int32_t maxr, int32_t dtype, void *stream);
+
+/* Global log-sum-exp merge of each request's partial outputs (replaces _merge,
+ * kernels.py:58-83, and its launch at kernels.py:166-167). */
+int ta_merge(const float *part, const float *lse, const int32_t *slots,
+             const int32_t *counts, void *out, int32_t nreq, int32_t hq,
+             int32_t d, int32_t maxs, int32_t dtype, void *stream);
+
+/* One decode-step attention layer on resident pools: every segment launch of
+ * the plan followed by the merge (replaces attention_matrix, kernels.py:152-168). */
+int ta_attention_matrix(const void *q, const void *kp, const void *vp,
+                        int32_t tcap, const ta_plan *plan, void *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TREE_ATTN_H */

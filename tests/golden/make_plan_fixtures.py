@@ -1,0 +1,147 @@
+"""Write exact planner outputs of the reference implementation as fixtures.
+
+The reference's published results pin plan *costs* and *job counts* only at
+default parameters.  This script imports the reference's pure-Python
+``tree.py`` / ``schedule.py`` (``src/tree_attention``) -- in the build
+container only, never on a GPU machine -- and records, for a set of trees and
+cost models, the full job list (requests and token runs, in order), the
+``estimated_us`` float and, for token-sequence trees, the node structure.
+
+    python tests/golden/make_plan_fixtures.py [/root/reference]
+
+Tree specs are stored with the fixtures, so the tests rebuild every tree with
+the build's own ``KVTree`` and compare plans field by field.
+"""
+import json
+import random
+import sys
+from pathlib import Path
+
+REF = Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+OUT = Path(__file__).resolve().parent / "plan_fixtures.json"
+sys.path.insert(0, str(REF / "src"))
+from tree_attention import KVTree, CostModel, schedule  # noqa: E402  (reference package)
+
+METHODS = ("request", "fixed", "greedy", "cube")
+MI355X_LIKE = [
+    dict(bandwidth=5.0e6, cube_flops=1.0e9, task_us=0.5, merge_us=0.01, cube_rows=16, key_tile=64,
+         kv_split=256, max_query_rows=512),
+    dict(bandwidth=4.2e6, cube_flops=6.0e8, task_us=1.25, merge_us=0.02, cube_rows=16, key_tile=64,
+         kv_split=1024, max_query_rows=256),
+]
+
+
+def runs(tokens):
+    out = []
+    for t in tokens:
+        if out and out[-1][0] + out[-1][1] == t:
+            out[-1][1] += 1
+        else:
+            out.append([t, 1])
+    return out
+
+
+def shared_prefix(requests, root, private):
+    tails = list(private) if isinstance(private, list) else [private] * requests
+    return [-1] + [0] * requests, [root] + tails, list(range(1, requests + 1))
+
+
+def nested_unequal():
+    parents, lengths = [-1], [4096]
+    for _ in range(8):
+        parents.append(0)
+        lengths.append(1024)
+    leaves = []
+    for child in range(1, 9):
+        for _ in range(4):
+            leaves.append(len(parents))
+            parents.append(child)
+            lengths.append(256)
+    return parents, lengths, leaves + [1, leaves[0], leaves[1]]
+
+
+def random_tree(rng):
+    n = rng.randint(2, 12)
+    parents, lengths = [-1], [rng.choice([0, 1, 7, 48, 300, 700, 1500])]
+    for i in range(1, n):
+        parents.append(rng.randrange(0, i))
+        lengths.append(rng.choice([1, 3, 16, 47, 64, 129, 500, 513, 1100]))
+    leaves = [i for i in range(n) if i not in parents[1:]] or [n - 1]
+    terminals = [rng.choice(leaves) for _ in range(rng.randint(1, 24))]
+    if rng.random() < 0.3:
+        terminals.append(rng.randrange(0, n))  # may end at an internal node
+    return parents, lengths, terminals
+
+
+def plan_record(tree, method, heads, model_kw):
+    model = CostModel(**model_kw)
+    plan = schedule(tree, heads[0], heads[1], heads[2], method, model)
+    return {"method": method, "heads": list(heads), "model": model_kw,
+            "estimated_us": plan.estimated_us,
+            "jobs": [[list(j.requests), runs(j.tokens)] for j in plan.jobs]}
+
+
+def tree_record(tree):
+    return {"storage_tokens": tree.storage_tokens,
+            "nodes": [[n.parent, runs(n.tokens), list(n.children), list(n.terminal), list(n.requests)]
+                      for n in tree.nodes],
+            "paths": [runs(p) for p in tree.paths]}
+
+
+def main():
+    cases = []
+
+    def add(name, kind, spec, heads=(32, 8, 128), models=({},), methods=METHODS):
+        tree = KVTree.synthetic(*spec) if kind == "synthetic" else KVTree.from_sequences(spec)
+        case = {"name": name, "kind": kind, "spec": spec, "tree": tree_record(tree), "plans": []}
+        for model_kw in models:
+            for method in methods:
+                case["plans"].append(plan_record(tree, method, heads, model_kw))
+        cases.append(case)
+
+    bench = {
+        "no_share": shared_prefix(32, 0, 1024),
+        "wide": shared_prefix(32, 2048, 64),
+        "unequal": shared_prefix(32, 1024, [32 + 31 * i for i in range(32)]),
+        "deep": ([-1, 0, 1, 1, 2, 2, 3, 3] + list(range(4, 8)) * 4, [512] * 8 + [64] * 16, list(range(8, 24))),
+        "wide_long": shared_prefix(128, 8128, 64),
+        "no_share_long": shared_prefix(128, 0, 8192),
+    }
+    for name, spec in bench.items():
+        add(name, "synthetic", spec, models=({},) + tuple(MI355X_LIKE) if name == "wide_long" else ({},))
+    add("cpu_baseline", "synthetic", shared_prefix(8, 1024, 64))
+    add("nested_unequal", "synthetic", nested_unequal(), models=({},) + tuple(MI355X_LIKE))
+    # tests/test_semantics.py trees, CostModel(kv_split=48), 8 Q / 2 KV heads, d = 32
+    for name, kind, spec in (
+            ("semantics_unequal", "sequences", [[1, 2, 3], [1, 2], [1, 2, 4, 5, 6], [7, 8], [1, 2, 3]]),
+            ("semantics_noshare", "sequences", [[1, 2, 3], [4], [5, 6, 7, 8, 9]]),
+            ("semantics_deep", "synthetic", ([-1, 0, 1, 1, 0], [129, 65, 17, 33, 81], [2, 3, 4]))):
+        add(name, kind, spec, heads=(8, 2, 32), models=({"kv_split": 48},))
+    # scripts/check_npu.py trees, CostModel(kv_split=128), 8 Q / 2 KV heads, d = 64
+    for name, kind, spec in (
+            ("npu_unequal", "synthetic", ([-1, 0, 0, 1, 1], [129, 65, 17, 33, 81], [2, 3, 4])),
+            ("npu_none", "sequences", [[1, 2, 3], [4], [5, 6, 7, 8, 9]]),
+            ("npu_duplicate_terminal", "sequences", [[1, 2], [1, 2], [1, 2, 3, 4], [1, 5, 6]]),
+            ("npu_wide", "synthetic", ([-1] + [0] * 32, [257] + [31 + i for i in range(32)], list(range(1, 33))))):
+        add(name, kind, spec, heads=(8, 2, 64), models=({"kv_split": 128},))
+    workloads = json.loads((REF / "configs/qwen_workloads.json").read_text())["workloads"]
+    for name, seqs in workloads.items():
+        add(f"qwen_{name}", "sequences", seqs, models=({}, MI355X_LIKE[0]))
+    rng = random.Random(20261201)
+    made = 0
+    while made < 40:
+        spec = random_tree(rng)
+        try:
+            KVTree.synthetic(*spec)
+        except ValueError:  # a request whose whole path has no tokens
+            continue
+        add(f"random_{made}", "synthetic", spec, models=({}, {"kv_split": 64, "max_query_rows": 16},
+                                                         MI355X_LIKE[made % 2]))
+        made += 1
+    OUT.write_text(json.dumps({"source": "reference src/tree_attention/{tree,schedule}.py", "cases": cases},
+                              separators=(",", ":")))
+    print(OUT, OUT.stat().st_size, len(cases))
+
+
+if __name__ == "__main__":
+    main()

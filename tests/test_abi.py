@@ -1,0 +1,60 @@
+"""The C-ABI library: loads, exports every declared symbol, struct layout agrees (no GPU calls)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from tree_attention import _native
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "tree_attn.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ta_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    names = declared_functions()
+    assert set(names) == set(_native.EXPORTS)
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.ta_version().decode().startswith("tree_attn gfx950")
+    assert b"16-byte" in lib.ta_error_string(1002)
+
+
+def test_library_rejects_bad_arguments_without_gpu_work():
+    lib = _native.load()
+    # unsupported head dim / dtype / null pointers are refused before any launch
+    assert lib.ta_merge(None, None, None, None, None, 1, 32, 96, 1, 0, None) == 1001
+    assert lib.ta_merge(None, None, None, None, None, 1, 32, 128, 1, 7, None) == 1003
+    assert lib.ta_segment(None, None, None, None, None, None, None, None, None, 1, 0, None, None,
+                          1, 32, 8, 128, 16, 1, 0, None) == 1001
+    assert lib.ta_segment(None, None, None, None, None, None, None, None, None, 1, 0, None, None,
+                          1, 30, 8, 128, 16, 1, 0, None) == 1001
+    assert lib.ta_attention_matrix(None, None, None, 1, None, None, None) == 1001
+
+
+def test_plan_struct_layout_matches_header(tmp_path):
+    fields = [f[0] for f in _native.TaPlan._fields_]
+    src = tmp_path / "layout.c"
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){",
+             'printf("%zu\\n", sizeof(ta_plan));']
+    lines += [f'printf("%zu\\n", offsetof(ta_plan, {f}));' for f in fields]
+    lines.append("return 0;}")
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(_native.TaPlan)
+    assert got[1:] == [getattr(_native.TaPlan, f).offset for f in fields]
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="not found"):
+        _native.load(tmp_path / "nope.so")

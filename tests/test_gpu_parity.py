@@ -1,0 +1,316 @@
+"""GPU parity of the HIP backend against the CPU FP32 oracle (reference src/tree_attention/reference.py).
+
+Tolerances are the reference's own device tolerances -- atol .006 / rtol .02
+(scripts/check_npu.py:29) for the small trees and atol .008 / rtol .03
+(scripts/benchmark.py:96) for the benchmark shapes -- plus the per-layer
+relative L2 bound of 0.3% against the FP32 oracle evaluated on the same
+(bf16/fp16-valued) Q/K/V.
+"""
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from oracle.attention_oracle import relative_l2, request_attention
+from tree_attention import CostModel, KVTree, schedule, shapes
+from tree_attention import _native
+from tree_attention.kernels import (CachedDecodePlan, attention, attention_matrix, merge, pack_kv, prepare,
+                                    segment)
+
+pytestmark = pytest.mark.gpu
+METHODS = ("request", "fixed", "greedy", "cube")
+REL_L2 = 3e-3
+MI355X_LIKE = CostModel(bandwidth=5.0e6, cube_flops=1.0e9, task_us=0.5, merge_us=0.01, cube_rows=16,
+                        key_tile=64, kv_split=256, max_query_rows=512)
+
+
+def say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+def make_inputs(tree, hq, hk, d, dtype, seed, tcap=None, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    t = tree.storage_tokens if tcap is None else tcap
+    q = (torch.randn(len(tree.paths), hq, d, generator=g) * scale).to(dtype)
+    k = torch.randn(t, hk, d, generator=g).to(dtype)
+    v = torch.randn(t, hk, d, generator=g).to(dtype)
+    return q, k, v
+
+
+def oracle_fp32(q, k, v, tree):
+    return request_attention(q.float(), k.float(), v.float(), tree)
+
+
+def check(out, ref32, atol, rtol, what):
+    ref = ref32.to(out.dtype)
+    err = relative_l2(out.cpu(), ref32)
+    torch.testing.assert_close(out.cpu(), ref, atol=atol, rtol=rtol, msg=lambda m: f"{what}: {m}")
+    assert err <= REL_L2, (what, err)
+    return err
+
+
+def run(tree, method, model, q, k, v, device, heads):
+    plan = schedule(tree, heads[0], heads[1], heads[2], method, model)
+    plan.validate(tree)
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    prepared = prepare(plan, qd)
+    out = attention_matrix(qd, kp, vp, prepared)
+    torch.cuda.synchronize()
+    return out
+
+
+SEMANTICS = {
+    "unequal": (lambda: KVTree.from_sequences([[1, 2, 3], [1, 2], [1, 2, 4, 5, 6], [7, 8], [1, 2, 3]]), 1.0),
+    "noshare": (lambda: KVTree.from_sequences([[1, 2, 3], [4], [5, 6, 7, 8, 9]]), 1.0),
+    "deep": (lambda: KVTree.synthetic([-1, 0, 1, 1, 0], [129, 65, 17, 33, 81], [2, 3, 4]), 30.0),
+}
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("name", list(SEMANTICS))
+def test_semantics_trees_d32(name, dtype, device):
+    """tests/test_semantics.py trees (8 Q / 2 KV heads, d=32, kv_split=48), incl. logits x30."""
+    build, scale = SEMANTICS[name]
+    tree = build()
+    q, k, v = make_inputs(tree, 8, 2, 32, dtype, 17, scale=scale)
+    ref = oracle_fp32(q, k, v, tree)
+    for method in METHODS:
+        say("semantics", name, dtype, method)
+        out = run(tree, method, CostModel(kv_split=48), q, k, v, device, (8, 2, 32))
+        check(out, ref, 0.006, 0.02, f"{name}/{method}")
+
+
+NPU_TREES = {
+    "unequal": lambda: KVTree.synthetic([-1, 0, 0, 1, 1], [129, 65, 17, 33, 81], [2, 3, 4]),
+    "none": lambda: KVTree.from_sequences([[1, 2, 3], [4], [5, 6, 7, 8, 9]]),
+    "duplicate_terminal": lambda: KVTree.from_sequences([[1, 2], [1, 2], [1, 2, 3, 4], [1, 5, 6]]),
+    "wide": lambda: KVTree.synthetic([-1] + [0] * 32, [257] + [31 + i for i in range(32)], list(range(1, 33))),
+}
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("name", list(NPU_TREES))
+def test_device_suite_d64(name, dtype, device):
+    """scripts/check_npu.py: 4 trees x {fp16, bf16} x 4 methods, 8 Q / 2 KV, d=64, kv_split=128."""
+    tree = NPU_TREES[name]()
+    q, k, v = make_inputs(tree, 8, 2, 64, dtype, 2026)
+    ref = oracle_fp32(q, k, v, tree)
+    for method in METHODS:
+        say("npu-suite", name, dtype, method)
+        out = run(tree, method, CostModel(kv_split=128), q, k, v, device, (8, 2, 64))
+        check(out, ref, 0.006, 0.02, f"{name}/{method}")
+
+
+@pytest.mark.parametrize("name", ["no_share", "wide", "unequal", "deep"])
+def test_benchmark_cases(name, device):
+    """scripts/benchmark.py shapes, bf16, 32 Q / 8 KV, d=128, default and MI355X-like cost models."""
+    tree = shapes.tree(shapes.benchmark_cases()[name])
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 101)
+    ref = oracle_fp32(q, k, v, tree)
+    for model in (CostModel(), MI355X_LIKE):
+        for method in METHODS:
+            say("bench-case", name, method, model.max_query_rows)
+            out = run(tree, method, model, q, k, v, device, (32, 8, 128))
+            check(out, ref, 0.008, 0.03, f"{name}/{method}")
+
+
+def test_headline_shape(device):
+    """128 requests x 8192 tokens, 8128 shared, bf16: rel-L2 <= 0.3% for cube (both models) and request."""
+    tree = shapes.tree(shapes.headline())
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 101)
+    say("headline oracle")
+    ref = oracle_fp32(q, k, v, tree)
+    errs = {}
+    for method, model in (("cube", CostModel()), ("cube", MI355X_LIKE), ("request", CostModel()),
+                          ("fixed", MI355X_LIKE)):
+        say("headline", method, model.max_query_rows)
+        out = run(tree, method, model, q, k, v, device, (32, 8, 128))
+        errs[(method, model.max_query_rows)] = check(out, ref, 0.008, 0.03, f"headline/{method}")
+    say("headline rel-L2", errs)
+
+
+def test_nested_unequal_tree(device):
+    """Root 4096 -> 8 x 1024 -> 4 x 256, an internal terminal and two duplicates; all methods."""
+    tree = shapes.tree(shapes.nested_unequal())
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 7)
+    ref = oracle_fp32(q, k, v, tree)
+    for model in (CostModel(), MI355X_LIKE):
+        for method in METHODS:
+            say("nested", method, model.max_query_rows)
+            out = run(tree, method, model, q, k, v, device, (32, 8, 128))
+            check(out, ref, 0.008, 0.03, f"nested/{method}")
+
+
+@pytest.mark.parametrize("hq,hk", [(8, 8), (16, 2), (32, 2), (64, 4)])
+def test_group_sizes(hq, hk, device):
+    """GQA group sizes 1, 8, 16, 16 (rows per request up to one full 16-row block)."""
+    tree = shapes.tree(shapes.shared_prefix(20, 300, [5 + 7 * i for i in range(20)]))
+    q, k, v = make_inputs(tree, hq, hk, 64, torch.bfloat16, 11)
+    ref = oracle_fp32(q, k, v, tree)
+    for method in METHODS:
+        say("group", hq, hk, method)
+        out = run(tree, method, CostModel(kv_split=100, max_query_rows=96), q, k, v, device, (hq, hk, 64))
+        check(out, ref, 0.008, 0.03, f"group{hq}/{hk}/{method}")
+
+
+def test_misaligned_pool_and_ragged_jobs(device):
+    """Odd pool capacity (rows not 16-byte aligned), odd job starts, 1-token jobs, partial tiles."""
+    tree = KVTree.synthetic([-1, 0, 0, 1, 1, 2, 0], [77, 1, 130, 3, 65, 200, 9], [3, 4, 5, 5, 6, 1])
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 5, tcap=tree.storage_tokens + 3)
+    ref = oracle_fp32(q, k, v, tree)
+    for model in (CostModel(kv_split=33), CostModel(kv_split=64, max_query_rows=8), MI355X_LIKE):
+        for method in METHODS:
+            say("ragged", method, model.kv_split)
+            out = run(tree, method, model, q, k, v, device, (32, 8, 128))
+            check(out, ref, 0.008, 0.03, f"ragged/{method}")
+
+
+def test_large_row_tiles_all_kinds(device):
+    """Jobs of 20, 40, 100 and 300 requests exercise the 64/128/256-row tile kernels."""
+    tree = KVTree.synthetic([-1, 0, 0, 0, 0], [700, 90, 33, 64, 129],
+                            [1] * 20 + [2] * 40 + [3] * 100 + [4] * 140)
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 9)
+    ref = oracle_fp32(q, k, v, tree)
+    for model in (CostModel(max_query_rows=1200, kv_split=512), CostModel(max_query_rows=256, kv_split=190)):
+        say("large-tiles", model.max_query_rows)
+        out = run(tree, "fixed", model, q, k, v, device, (32, 8, 128))
+        check(out, ref, 0.008, 0.03, "large-tiles")
+
+
+def test_attention_packs_and_c_abi_phases_agree(device):
+    """attention(q,k,v) == attention_matrix on packed pools == explicit ta_segment + ta_merge calls."""
+    tree = shapes.tree(shapes.benchmark_cases()["deep"])
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 3)
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    prepared = prepare(schedule(tree, method="cube"), qd)
+    a = attention(qd, kd, vd, prepared).clone()
+    kp, vp = pack_kv(kd, vd)
+    b = attention_matrix(qd, kp, vp, prepared).clone()
+    prepared.out.zero_()
+    for kind in range(4):
+        segment(qd, kp, vp, prepared, kind)
+    c = merge(prepared).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(b, c)
+
+
+def test_cached_decode_plan_steps(device):
+    """scripts/benchmark_decode_plan.py protocol: 32 req, 1024 + 64 prompt, growing tails, check steps."""
+    base = shapes.tree(shapes.shared_prefix(32, 1024, 64))
+    prefix = base.storage_tokens
+    steps = 16
+    g = torch.Generator().manual_seed(301)
+    q = torch.randn(32, 32, 128, generator=g).bfloat16()
+    k = torch.randn(prefix + 32 * steps, 8, 128, generator=g).bfloat16()
+    v = torch.randn(prefix + 32 * steps, 8, 128, generator=g).bfloat16()
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    for method in ("fixed", "cube"):
+        cached = CachedDecodePlan(schedule(base, method=method), qd, prefix, steps)
+        for step in (0, 7, steps - 1):
+            say("decode", method, step)
+            out = attention_matrix(qd, kp, vp, cached.update(step + 1)).cpu()
+            paths = [p + tuple(prefix + r * steps + t for t in range(step + 1)) for r, p in enumerate(base.paths)]
+            ref = oracle_fp32(q, k, v, KVTree([], paths))
+            check(out, ref, 0.008, 0.03, f"decode/{method}/{step}")
+        # zero generated tokens: tails contribute nothing (reference leaves this undefined)
+        out = attention_matrix(qd, kp, vp, cached.update(0)).cpu()
+        check(out, oracle_fp32(q, k, v, base), 0.008, 0.03, f"decode/{method}/empty-tail")
+
+
+def test_reuse_across_calls_and_streams(device):
+    """prepared.out is overwritten per call; launches follow torch's current stream."""
+    tree = shapes.tree(shapes.benchmark_cases()["wide"])
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 1)
+    q2 = torch.flip(q, [0]).contiguous()
+    qd, q2d = q.to(device), q2.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    prepared = prepare(schedule(tree, method="cube"), qd)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        out1 = attention_matrix(qd, kp, vp, prepared).clone()
+        out2 = attention_matrix(q2d, kp, vp, prepared).clone()
+    s.synchronize()
+    check(out1, oracle_fp32(q, k, v, tree), 0.008, 0.03, "stream/1")
+    check(out2, oracle_fp32(q2, k, v, tree), 0.008, 0.03, "stream/2")
+
+
+def test_full_size_properties(device):
+    """Headline size: equal keys give the path mean of V; permuting requests permutes outputs."""
+    tree = shapes.tree(shapes.headline())
+    g = torch.Generator().manual_seed(4)
+    t = tree.storage_tokens
+    q = torch.randn(128, 32, 128, generator=g).bfloat16()
+    k = torch.ones(t, 8, 128).bfloat16()
+    v = torch.randn(t, 8, 128, generator=g).bfloat16()
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    prepared = prepare(schedule(tree, 32, 8, 128, "cube", MI355X_LIKE), qd)
+    out = attention_matrix(qd, kp, vp, prepared).float().cpu()
+    vf = v.float()
+    root_sum = vf[:8128].sum(0)
+    for r in (0, 63, 127):
+        mean = (root_sum + vf[8128 + 64 * r: 8128 + 64 * (r + 1)].sum(0)) / 8192
+        torch.testing.assert_close(out[r], mean.repeat_interleave(4, 0), atol=4e-3, rtol=0.02)
+    # request permutation equivariance (the tree is symmetric in its requests)
+    perm = torch.randperm(128, generator=g)
+    k2 = torch.randn(t, 8, 128, generator=g).bfloat16()
+    kp2, _ = pack_kv(k2.to(device), v.to(device))
+    a = attention_matrix(qd, kp2, vp, prepared).clone()
+    # swapping request r's query with request perm[r] and its private KV rows with perm[r]'s
+    idx = torch.arange(t)
+    for r in range(128):
+        idx[8128 + 64 * r: 8128 + 64 * (r + 1)] = torch.arange(8128 + 64 * perm[r], 8128 + 64 * (perm[r] + 1))
+    kp3, vp3 = pack_kv(k2[idx].to(device), v[idx].to(device))
+    b = attention_matrix(q[perm].contiguous().to(device), kp3, vp3, prepared).clone()
+    torch.cuda.synchronize()
+    assert relative_l2(b.cpu(), a[perm.to(device)].cpu()) < 1e-6
+
+
+def test_bad_inputs_raise(device):
+    tree = shapes.tree(shapes.benchmark_cases()["wide"])
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 1)
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    prepared = prepare(schedule(tree, method="cube"), qd)
+    with pytest.raises(ValueError):
+        attention_matrix(qd.half(), kp, vp, prepared)
+    with pytest.raises(ValueError):
+        attention_matrix(qd[:3], kp, vp, prepared)
+    with pytest.raises(ValueError):
+        attention_matrix(qd, kp.transpose(1, 2), vp, prepared)
+    lib = _native.load()
+    bad = ctypes.c_void_p(qd.data_ptr() + 2)
+    rc = lib.ta_attention_matrix(bad, kp.data_ptr(), vp.data_ptr(), kp.shape[2], ctypes.byref(prepared.abi),
+                                 prepared.out.data_ptr(), None)
+    assert rc == 1002
+
+
+def test_graph_replay_matches_eager(device):
+    """A captured layer replays to the eager result every time, with eager work in between."""
+    tree = shapes.tree(shapes.benchmark_cases()["unequal"])
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 12)
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    prepared = prepare(schedule(tree, method="cube"), qd)
+    eager = attention_matrix(qd, kp, vp, prepared).clone()
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        attention_matrix(qd, kp, vp, prepared)
+    stream.wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        captured = attention_matrix(qd, kp, vp, prepared).clone()
+    for rep in range(4):
+        prepared.out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), rep
+        other = attention_matrix(torch.flip(qd, [0]).contiguous(), kp, vp, prepared).clone()
+        torch.cuda.synchronize()
+        assert not torch.equal(other, eager)

@@ -1,0 +1,218 @@
+"""Planner parity with the reference (src/tree_attention/schedule.py).
+
+Pinned by the reference's published results (float-exact ``estimated_us`` and
+job counts) and by plans the reference implementation produced for the same
+trees and cost parameters (tests/golden/make_plan_fixtures.py).
+"""
+import gc
+import json
+import weakref
+from pathlib import Path
+
+import pytest
+
+from tree_attention import CostModel, KVTree, schedule, shapes
+from tree_attention.schedule import Plan, physical_jobs
+
+GOLDEN = Path(__file__).parent / "golden"
+METHODS = ("request", "fixed", "greedy", "cube")
+
+
+def _load(name):
+    return json.loads((GOLDEN / name).read_text())
+
+
+def _runs(tokens):
+    out = []
+    for t in tokens:
+        if out and out[-1][0] + out[-1][1] == t:
+            out[-1][1] += 1
+        else:
+            out.append([t, 1])
+    return out
+
+
+def test_reference_grid_costs_bit_exact():
+    """results/tree_grid_run{1,2,3}.json: 81 trees x 4 methods, default CostModel."""
+    rows = _load("planner_tree_grid.json")["rows"]
+    i = 0
+    for params, spec in shapes.reference_grid():
+        tree = shapes.tree(spec)
+        for method in METHODS:
+            row = rows[i]
+            i += 1
+            assert row["shape"] == params and row["method"] == method
+            plan = schedule(tree, method=method)
+            plan.validate(tree)
+            assert plan.estimated_us == row["estimated_us"], (params, method)
+            assert len(plan.jobs) == row["logical_jobs"]
+            assert len(physical_jobs(plan.jobs)) == row["jobs"]
+            assert tree.storage_tokens == row["storage_tokens"]
+    assert i == 324
+
+
+def test_tree_scan_costs_and_choices():
+    """results/tree_scan.json: 81 small trees, costs, job counts, whether cube differs."""
+    for row in _load("planner_tree_scan.json")["rows"]:
+        tree = KVTree.synthetic([-1, 0, 0, 1, 1, 2, 2], row["lengths"], [3, 4, 5, 6])
+        plans = {m: schedule(tree, method=m) for m in METHODS}
+        norm = {m: sorted((j.requests, j.tokens) for j in p.jobs) for m, p in plans.items()}
+        for m, p in plans.items():
+            assert p.estimated_us == row["cost_us"][m], (row["lengths"], m)
+            assert len(p.jobs) == row["jobs"][m]
+        assert (norm["cube"] != norm["fixed"]) == row["cube_differs_fixed"]
+        assert (norm["cube"] != norm["greedy"]) == row["cube_differs_greedy"]
+
+
+def test_benchmark_case_job_counts():
+    """results/benchmark.json: physical job counts and token counts of the six cases."""
+    cases = shapes.benchmark_cases()
+    for row in _load("benchmark_cases.json")["rows"]:
+        if row["method"].startswith("vendor"):
+            continue
+        tree = shapes.tree(cases[row["case"]])
+        plan = schedule(tree, 32, 8, 128, row["method"])
+        assert len(physical_jobs(plan.jobs)) == row["jobs"], (row["case"], row["method"])
+        assert tree.storage_tokens == row["shared_tokens"]
+        assert sum(map(len, tree.paths)) == row["logical_tokens"]
+
+
+def test_npu_correctness_logical_jobs():
+    """results/npu_correctness.json: logical jobs with CostModel(kv_split=128), 8 Q / 2 KV, d=64."""
+    trees = {
+        "unequal": KVTree.synthetic([-1, 0, 0, 1, 1], [129, 65, 17, 33, 81], [2, 3, 4]),
+        "none": KVTree.from_sequences([[1, 2, 3], [4], [5, 6, 7, 8, 9]]),
+        "duplicate_terminal": KVTree.from_sequences([[1, 2], [1, 2], [1, 2, 3, 4], [1, 5, 6]]),
+        "wide": KVTree.synthetic([-1] + [0] * 32, [257] + [31 + i for i in range(32)], list(range(1, 33))),
+    }
+    for row in _load("npu_correctness_jobs.json")["rows"]:
+        plan = schedule(trees[row["case"]], 8, 2, 64, row["method"], CostModel(kv_split=128))
+        assert len(plan.jobs) == row["logical_jobs"], row
+
+
+def test_plans_match_reference_implementation():
+    """Exact job tuples, job order and estimated_us, including non-default parameters."""
+    data = _load("plan_fixtures.json")
+    n = 0
+    for case in data["cases"]:
+        tree = (KVTree.from_sequences(case["spec"]) if case["kind"] == "sequences"
+                else KVTree.synthetic(*case["spec"]))
+        for want in case["plans"]:
+            q, k, d = want["heads"]
+            plan = schedule(tree, q, k, d, want["method"], CostModel(**want["model"]))
+            got = [[list(j.requests), _runs(j.tokens)] for j in plan.jobs]
+            assert got == want["jobs"], (case["name"], want["method"], want["model"])
+            assert plan.estimated_us == want["estimated_us"], (case["name"], want["method"], want["model"])
+            assert plan.settings == {**CostModel(**want["model"]).__dict__, "qheads": q, "kvheads": k,
+                                     "head_dim": d}
+            n += 1
+    assert n > 400
+
+
+def test_dynamic_plan_not_worse_than_greedy():
+    """tests/test_semantics.py:45-54."""
+    for root in (16, 128, 1024):
+        for child in (8, 64, 256):
+            for leaf in (16, 128, 512):
+                tree = KVTree.synthetic([-1, 0, 0, 1, 1, 2, 2],
+                                        [root, child, child, leaf, 2 * leaf, leaf, 2 * leaf], [3, 4, 5, 6])
+                greedy = schedule(tree, method="greedy")
+                dynamic = schedule(tree, method="cube")
+                dynamic.validate(tree)
+                assert dynamic.estimated_us <= greedy.estimated_us + 1e-10
+
+
+def test_dp_optimal_against_brute_force():
+    """Cube DP equals the minimum over every push/no-push assignment on small trees."""
+    from itertools import product as iproduct
+    for lengths in ([16, 8, 8, 16, 16, 16, 16], [1024, 64, 256, 128, 512, 16, 128], [128, 8, 256, 512, 16, 512, 128]):
+        tree = KVTree.synthetic([-1, 0, 0, 1, 1, 2, 2], lengths, [3, 4, 5, 6])
+        model = CostModel()
+        best = None
+        # pushed decisions for nodes 1..6 (pushing = child joins parent's chain)
+        for choice in iproduct((0, 1), repeat=6):
+            jobs = _jobs_for_choice(tree, choice, model)
+            cost = 0
+            for j in physical_jobs(jobs):
+                cost = cost + model.cost(j.requests, j.tokens, 32, 8, 128)
+            best = cost if best is None or cost < best else best
+        plan = schedule(tree, method="cube")
+        assert abs(plan.estimated_us - best) <= 1e-9 * best, lengths
+
+
+def _jobs_for_choice(tree, pushed, model):
+    """Jobs of an arbitrary push assignment (pushed[c-1] for node c), default tiling."""
+    from tree_attention.schedule import Job
+    req_tile = max(1, model.max_query_rows // 4)
+
+    def split(reqs, toks):
+        return [Job(tuple(reqs[a:a + req_tile]), tuple(toks[b:b + model.kv_split]))
+                for a in range(0, len(reqs), req_tile) for b in range(0, len(toks), model.kv_split)]
+    jobs = []
+
+    def walk(v, inherited):
+        node = tree.nodes[v]
+        toks = inherited + node.tokens
+        detached = set()
+        for c in node.children:
+            if pushed[c - 1]:
+                detached.update(tree.nodes[c].requests)
+        jobs.extend(split(tuple(r for r in node.requests if r not in detached), toks))
+        for c in node.children:
+            walk(c, toks if pushed[c - 1] else ())
+    walk(0, ())
+    return jobs
+
+
+def test_schedule_releases_input_tree():
+    """tests/test_semantics.py:56-67 (gc disabled: no reference cycles may hold the tree)."""
+    gc.disable()
+    try:
+        for method in METHODS:
+            tree = KVTree.from_sequences([[1, 2, 3], [1, 2, 4]])
+            ref = weakref.ref(tree)
+            plan = schedule(tree, method=method)
+            del tree
+            assert ref() is None, method
+            assert plan.jobs
+    finally:
+        gc.enable()
+
+
+def test_plan_detects_double_counting():
+    """tests/test_semantics.py:69-74."""
+    tree = KVTree.from_sequences([[1, 2], [1, 3]])
+    plan = schedule(tree)
+    plan.jobs.append(plan.jobs[0])
+    with pytest.raises(ValueError):
+        plan.validate(tree)
+
+
+def test_errors():
+    tree = KVTree.from_sequences([[1, 2], [1, 3]])
+    with pytest.raises(ValueError):
+        schedule(tree, 30, 8)
+    with pytest.raises(ValueError):
+        schedule(tree, method="bogus")
+
+
+def test_all_methods_partition_physical_plans():
+    for name, spec in shapes.benchmark_cases().items():
+        if name.endswith("_long"):
+            continue
+        tree = shapes.tree(spec)
+        for method in METHODS:
+            plan = schedule(tree, method=method)
+            plan.validate(tree)
+            Plan(physical_jobs(plan.jobs), method, plan.estimated_us, plan.settings).validate(tree)
+
+
+def test_subclassed_cost_model_is_honoured():
+    """A CostModel subclass overriding cost() takes the literal (unaccelerated) path."""
+    class Flat(CostModel):
+        def cost(self, requests, tokens, qheads, kvheads, dim):
+            return float(len(tokens)) if requests and tokens else 0.0
+    tree = KVTree.synthetic([-1, 0, 0], [100, 10, 10], [1, 2])
+    plan = schedule(tree, method="cube", model=Flat())
+    assert plan.estimated_us == 120.0  # sharing the root is cheapest
+    plan.validate(tree)

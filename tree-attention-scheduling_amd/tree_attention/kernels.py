@@ -1,0 +1,272 @@
+"""Execution backend: plan lowering plus the HIP segment / merge kernels.
+
+Drop-in for the reference's ``src/tree_attention/kernels.py``: ``PreparedPlan``
+(:86-100), ``prepare`` (:103-141), ``pack_kv`` (:144-145), ``attention``
+(:148-149), ``attention_matrix`` (:152-168) and ``CachedDecodePlan``
+(:171-186) keep their names, arguments and results.  The Triton kernels are
+replaced by the gfx950 library ``libtree_attn.so`` (include/tree_attn.h),
+called through ctypes on torch's current HIP stream.  There is no CPU or
+PyTorch fallback: without the library every call raises ``RuntimeError``.
+
+Internal layout (the build's own; only ``out`` is contractual):
+
+* ``qids [J, MAXR]``, ``kids [J, 1]`` (first physical token), ``qlen [J]``,
+  ``klen [J]`` as in the reference (kernels.py:114-128); jobs are the plan's
+  physical jobs, stably sorted small-first exactly like the reference
+  (kernels.py:109-110) so ``CachedDecodePlan.tail_indices`` match.
+* Partial outputs are compact: job ``j``'s requests own partial rows
+  ``rowbase[j] .. rowbase[j] + qlen[j]`` of ``part [NSLOT, HQ, D]`` and
+  ``lse [NSLOT, HQ]``; ``slots[r]`` lists request ``r``'s partial rows in job
+  order (the reference instead indexes ``job * MAXR + local``, which allocates
+  ``J * MAXR`` rows).
+* Work items: small jobs (<= 16 query rows) are processed one workgroup per
+  (job, KV head); larger jobs are cut into 64/128/256-row tiles, one
+  workgroup per (job, tile, KV head).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import _native
+from .schedule import Job, Plan, physical_jobs
+
+_DTYPES = {torch.bfloat16: _native.TA_BF16, torch.float16: _native.TA_FP16}
+SMALL_ROWS = 16  # rows of one MFMA block; same threshold as kernels.py:109-110
+
+
+def _large_kind(rows: int) -> int:
+    if rows <= 64:
+        return _native.TA_LARGE64
+    if rows <= 128:
+        return _native.TA_LARGE128
+    return _native.TA_LARGE256
+
+
+@dataclass
+class PreparedPlan:
+    """Device metadata and reusable scratch of one plan (reference kernels.py:86-100)."""
+    jobs: list
+    small_jobs: int
+    contiguous_k: bool
+    contiguous_q: bool
+    qids: torch.Tensor
+    kids: torch.Tensor
+    qlen: torch.Tensor
+    klen: torch.Tensor
+    slots: torch.Tensor
+    counts: torch.Tensor
+    part: torch.Tensor
+    lse: torch.Tensor
+    out: torch.Tensor
+    rowbase: torch.Tensor | None = None
+    items: dict = field(default_factory=dict)
+    abi: _native.TaPlan | None = None
+    metadata: torch.Tensor | None = None
+
+
+def _build_items(jobs, small_jobs, group, kvheads):
+    """Work items per kernel kind as int32 arrays (see module docstring)."""
+    small = np.arange(small_jobs, dtype=np.int32)
+    large = {k: [] for k in _native.KIND_ROWS}
+    for j in range(small_jobs, len(jobs)):
+        rows = len(jobs[j].requests) * group
+        kind = _large_kind(rows)
+        tile = _native.KIND_ROWS[kind]
+        for h in range(kvheads):
+            for row0 in range(0, rows, tile):
+                large[kind].append((j, row0, h))
+    items = {_native.TA_SMALL: small}
+    for kind, triples in large.items():
+        items[kind] = np.asarray(triples, dtype=np.int32).reshape(-1)
+    return items
+
+
+def prepare(plan: Plan, q: torch.Tensor) -> PreparedPlan:
+    """Lower ``plan`` to device metadata and scratch for queries shaped like ``q``.
+
+    Mirrors kernels.py:103-141: physical jobs, stable small-first order, one
+    host-to-device copy of all int32 metadata, scratch allocated once.  Raises
+    ``ValueError`` for jobs without requests or tokens, request ids outside
+    ``q`` and token runs that are not consecutive physical ids.
+    """
+    if q.dim() != 3:
+        raise ValueError("q must be [requests, query heads, head dim]")
+    nreq, hq, dim = q.shape
+    kvheads = plan.settings["kvheads"]
+    if hq % kvheads:
+        raise ValueError("Query heads must be divisible by KV heads")
+    group = hq // kvheads
+    jobs = physical_jobs(plan.jobs)
+    jobs.sort(key=lambda job: len(job.requests) * group > SMALL_ROWS)
+    small_jobs = sum(len(job.requests) * group <= SMALL_ROWS for job in jobs)
+    if not jobs:
+        raise ValueError("Plan has no jobs")
+    njobs = len(jobs)
+    maxr = max(len(j.requests) for j in jobs)
+    qids = np.zeros((njobs, maxr), dtype=np.int32)
+    kids = np.zeros((njobs, 1), dtype=np.int32)
+    qlen = np.zeros(njobs, dtype=np.int32)
+    klen = np.zeros(njobs, dtype=np.int32)
+    rowbase = np.zeros(njobs, dtype=np.int32)
+    slots = [[] for _ in range(nreq)]
+    nslot = 0
+    for i, job in enumerate(jobs):
+        reqs, toks = job.requests, job.tokens
+        if not reqs or not toks:
+            raise ValueError("Every job needs requests and tokens")
+        if toks[-1] - toks[0] + 1 != len(toks) or toks[0] < 0 or (
+                len(toks) > 1 and toks != tuple(range(toks[0], toks[0] + len(toks)))):
+            raise ValueError(f"Job {i} tokens are not one run of consecutive physical ids")
+        qids[i, :len(reqs)] = reqs
+        kids[i, 0] = toks[0]
+        qlen[i] = len(reqs)
+        klen[i] = len(toks)
+        rowbase[i] = nslot
+        for local, r in enumerate(reqs):
+            if not 0 <= r < nreq:
+                raise ValueError(f"Job {i} names request {r} outside q's {nreq} requests")
+            slots[r].append(nslot + local)
+        nslot += len(reqs)
+    maxs = max(1, max(map(len, slots)))
+    slot_array = np.zeros((nreq, maxs), dtype=np.int32)
+    for r, values in enumerate(slots):
+        slot_array[r, :len(values)] = values
+    counts = np.array([len(s) for s in slots], dtype=np.int32)
+    items = _build_items(jobs, small_jobs, group, kvheads)
+
+    arrays = [qids, kids, qlen, klen, slot_array, counts, rowbase] + [items[k] for k in sorted(items)]
+    dev = q.device
+    metadata = torch.from_numpy(np.concatenate([a.ravel() for a in arrays])).to(dev)
+    views, offset = [], 0
+    for array in arrays:
+        views.append(metadata[offset:offset + array.size].view(array.shape))
+        offset += array.size
+    qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t = views[:7]
+    item_views = dict(zip(sorted(items), views[7:]))
+    contiguous_q = all(j.requests[-1] - j.requests[0] + 1 == len(j.requests) for j in jobs)
+    part = torch.empty((nslot, hq, dim), device=dev, dtype=torch.float32)
+    lse = torch.empty((nslot, hq), device=dev, dtype=torch.float32)
+    out = torch.empty_like(q)
+
+    abi = _native.TaPlan()
+    abi.qids, abi.kstart, abi.qlen, abi.klen = (qids_t.data_ptr(), kids_t.data_ptr(),
+                                                qlen_t.data_ptr(), klen_t.data_ptr())
+    abi.rowbase, abi.slots, abi.counts = rowbase_t.data_ptr(), slots_t.data_ptr(), counts_t.data_ptr()
+    for kind, view in item_views.items():
+        abi.items[kind] = view.data_ptr() if view.numel() else None
+        per = 1 if kind == _native.TA_SMALL else 3
+        abi.n_items[kind] = view.numel() // per
+    abi.part, abi.lse = part.data_ptr(), lse.data_ptr()
+    abi.njobs, abi.maxr, abi.maxs, abi.nreq, abi.nslot = njobs, maxr, maxs, nreq, nslot
+    abi.hq, abi.hk, abi.d = hq, kvheads, dim
+    abi.dtype = _DTYPES.get(q.dtype, -1)
+    return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
+                        slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata)
+
+
+def pack_kv(k: torch.Tensor, v: torch.Tensor):
+    """``k [T,HK,D] -> kp [HK,D,T]`` (token-minor) and ``v -> vp [HK,T,D]`` (kernels.py:144-145)."""
+    return k.permute(1, 2, 0).contiguous(), v.permute(1, 0, 2).contiguous()
+
+
+def attention(q, k, v, prepared):
+    """``attention_matrix`` on pools packed from ``k, v [T,HK,D]`` (kernels.py:148-149)."""
+    return attention_matrix(q, *pack_kv(k, v), prepared)
+
+
+def _check_inputs(q, kp, vp, p):
+    abi = p.abi
+    if q.dtype not in _DTYPES or kp.dtype != q.dtype or vp.dtype != q.dtype:
+        raise ValueError("q, kp and vp must share dtype bfloat16 or float16")
+    if _DTYPES[q.dtype] != abi.dtype:
+        raise ValueError("q dtype differs from the dtype the plan was prepared for")
+    if not (q.is_cuda and kp.device == q.device and vp.device == q.device):
+        raise ValueError("q, kp and vp must be on the same GPU")
+    if tuple(q.shape) != (abi.nreq, abi.hq, abi.d):
+        raise ValueError(f"q shape {tuple(q.shape)} differs from the prepared {(abi.nreq, abi.hq, abi.d)}")
+    if kp.dim() != 3 or vp.dim() != 3 or kp.shape[0] != abi.hk or kp.shape[1] != abi.d:
+        raise ValueError("kp must be [KV heads, head dim, tokens]")
+    if tuple(vp.shape) != (abi.hk, kp.shape[2], abi.d):
+        raise ValueError("vp must be [KV heads, tokens, head dim] with kp's token capacity")
+    if not (kp.is_contiguous() and vp.is_contiguous()):
+        raise ValueError("kp and vp must be contiguous")
+
+
+def attention_matrix(q, kp, vp, prepared):
+    """Attention on resident ``K [HK,D,T]`` / ``V [HK,T,D]`` pools (kernels.py:152-168).
+
+    Returns ``prepared.out`` (``[R, HQ, D]`` in q's dtype), which every call
+    overwrites, as in the reference.
+    """
+    p = prepared
+    _check_inputs(q, kp, vp, p)
+    if not q.is_contiguous():
+        q = q.contiguous()
+    lib = _native.load()
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.ta_attention_matrix(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), kp.shape[2],
+                                     ctypes.byref(p.abi), p.out.data_ptr(), stream)
+    _native.check(rc)
+    return p.out
+
+
+def segment(q, kp, vp, prepared, kind: int):
+    """Launch one segment phase (``kind`` = TA_SMALL / TA_LARGE64/128/256) of a plan.
+
+    Counterpart of the direct ``_segment`` launches in the reference's
+    scripts/calibrate_tiles.py:24-29 and scripts/profile_kernel.py:17-20.
+    """
+    p = prepared
+    _check_inputs(q, kp, vp, p)
+    abi = p.abi
+    n = abi.n_items[kind]
+    if n == 0:
+        return
+    lib = _native.load()
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.ta_segment(q.contiguous().data_ptr(), kp.data_ptr(), vp.data_ptr(), abi.qids, abi.kstart,
+                            abi.qlen, abi.klen, abi.rowbase, abi.items[kind], n, kind, abi.part, abi.lse,
+                            abi.nreq, abi.hq, abi.hk, abi.d, kp.shape[2], abi.maxr, abi.dtype, stream)
+    _native.check(rc)
+
+
+def merge(prepared):
+    """Launch the log-sum-exp merge of a plan's partials into ``prepared.out`` (kernels.py:166-167)."""
+    p = prepared
+    abi = p.abi
+    lib = _native.load()
+    with torch.cuda.device(p.out.device):
+        stream = torch.cuda.current_stream(p.out.device).cuda_stream
+        rc = lib.ta_merge(abi.part, abi.lse, abi.slots, abi.counts, p.out.data_ptr(), abi.nreq, abi.hq,
+                          abi.d, abi.maxs, abi.dtype, stream)
+    _native.check(rc)
+    return p.out
+
+
+class CachedDecodePlan:
+    """A prompt schedule plus one contiguous growing KV tail per request (kernels.py:171-186)."""
+
+    def __init__(self, prefix_plan, q, prefix_tokens, max_new_tokens):
+        tails = [Job((r,), tuple(range(prefix_tokens + r * max_new_tokens,
+                                       prefix_tokens + (r + 1) * max_new_tokens)))
+                 for r in range(q.shape[0])]
+        plan = Plan(prefix_plan.jobs + tails, prefix_plan.method, prefix_plan.estimated_us,
+                    prefix_plan.settings)
+        self.max_new_tokens = max_new_tokens
+        self.prepared = prepare(plan, q)
+        ordered = self.prepared.jobs
+        self.tail_indices = torch.tensor([i for i, job in enumerate(ordered) if job.tokens[0] >= prefix_tokens],
+                                         device=q.device)
+
+    def update(self, generated_tokens):
+        """Set every tail's length to ``generated_tokens`` (device-side fill, no sync)."""
+        if not 0 <= generated_tokens <= self.max_new_tokens:
+            raise ValueError("generated_tokens must be within [0, max_new_tokens]")
+        self.prepared.klen.index_fill_(0, self.tail_indices, generated_tokens)
+        return self.prepared

@@ -1,0 +1,133 @@
+"""Named tree shapes of the reference's benchmarks and of the evaluation configs.
+
+Each function returns the ``(parents, lengths, terminals)`` triple accepted by
+``KVTree.synthetic``; ``tree(spec)`` builds it.
+
+* ``benchmark_cases`` -- scripts/benchmark.py:14-23 (``wide_long`` is the
+  128-request x 8192-token, 8128-shared headline shape).
+* ``reference_grid`` -- the reference's 81 evaluation trees,
+  scripts/tree_shapes.py:5-19.
+* ``config_grid`` -- the 81-shape factorial grid requests x context x shared
+  fraction x depth.  ``shared = floor(fraction * context + 0.5)``; the shared
+  region is cut into ``depth`` levels of a balanced binary tree (level ``i``
+  has ``2**i`` nodes), level lengths ``shared // depth`` with the first
+  ``shared % depth`` levels one token longer; requests are spread evenly over
+  the last level's nodes (request ``r`` goes to leaf ``r * leaves // R``) and
+  each gets a private tail of ``context - shared`` tokens.
+* ``nested_unequal`` -- root 4096 -> 8 x 1024 -> 4 x 256 per child (32 leaf
+  requests), plus one request ending at the first 1024-token node and two
+  requests duplicating the first two leaf paths (35 requests, 20,480 tokens).
+* ``calibration_grid`` -- shapes used only to fit the MI355X cost model; every
+  length is disjoint from the evaluation shapes above.
+"""
+from __future__ import annotations
+
+from itertools import product
+
+from .tree import KVTree
+
+
+def tree(spec) -> KVTree:
+    parents, lengths, terminals = spec
+    return KVTree.synthetic(list(parents), list(lengths), list(terminals))
+
+
+def shared_prefix(requests: int, root: int, private) -> tuple:
+    """One shared root of ``root`` tokens plus a private child per request."""
+    tails = list(private) if isinstance(private, (list, tuple)) else [private] * requests
+    return [-1] + [0] * requests, [root] + tails, list(range(1, requests + 1))
+
+
+def benchmark_cases() -> dict:
+    """The six representative shapes of scripts/benchmark.py:14-23."""
+    return {
+        "no_share": shared_prefix(32, 0, 1024),
+        "wide": shared_prefix(32, 2048, 64),
+        "unequal": shared_prefix(32, 1024, [32 + 31 * i for i in range(32)]),
+        "deep": ([-1, 0, 1, 1, 2, 2, 3, 3] + list(range(4, 8)) * 4, [512] * 8 + [64] * 16,
+                 list(range(8, 24))),
+        "wide_long": shared_prefix(128, 8128, 64),
+        "no_share_long": shared_prefix(128, 0, 8192),
+    }
+
+
+def headline() -> tuple:
+    """128 requests x 8192 tokens, 8128 shared (16,320 physical tokens)."""
+    return shared_prefix(128, 8128, 64)
+
+
+def cpu_baseline_shape() -> tuple:
+    """8 requests, 1024-token shared root plus 64 private tokens each."""
+    return shared_prefix(8, 1024, 64)
+
+
+def nested_unequal() -> tuple:
+    parents, lengths = [-1], [4096]
+    for _ in range(8):
+        parents.append(0)
+        lengths.append(1024)
+    leaves = []
+    for child in range(1, 9):
+        for _ in range(4):
+            leaves.append(len(parents))
+            parents.append(child)
+            lengths.append(256)
+    terminals = leaves + [1, leaves[0], leaves[1]]
+    return parents, lengths, terminals
+
+
+def reference_grid():
+    """Yield ``(params, spec)`` for scripts/tree_shapes.py:5-19's 81 trees."""
+    for fanout, root, shared, private in product(((3, 1), (9, 3), (17, 7)), (32, 192, 768),
+                                                (12, 96, 384), (24, 192, 768)):
+        parents, lengths, terminals = [-1], [root], []
+        for branch, width in enumerate(fanout):
+            node = len(parents)
+            parents.append(0)
+            lengths.append(shared * (branch + 1) + 7 * branch)
+            for leaf in range(width):
+                terminals.append(len(parents))
+                parents.append(node)
+                lengths.append(private * (1 + leaf % 3) + 5 * branch)
+        yield dict(fanout=list(fanout), root=root, shared=shared, private=private), (parents, lengths, terminals)
+
+
+def grid_tree(requests: int, context: int, fraction: float, depth: int) -> tuple:
+    shared = int(fraction * context + 0.5)
+    private = context - shared
+    level_len = [shared // depth + (1 if i < shared % depth else 0) for i in range(depth)]
+    parents, lengths = [-1], [level_len[0]]
+    level = [0]
+    for i in range(1, depth):
+        nxt = []
+        for parent in level:
+            for _ in range(2):
+                nxt.append(len(parents))
+                parents.append(parent)
+                lengths.append(level_len[i])
+        level = nxt
+    terminals = []
+    for r in range(requests):
+        leaf = level[r * len(level) // requests]
+        terminals.append(len(parents))
+        parents.append(leaf)
+        lengths.append(private)
+    return parents, lengths, terminals
+
+
+def config_grid():
+    """Yield ``(params, spec)`` for the 81-shape requests x context x fraction x depth grid."""
+    for requests, context, fraction, depth in product((16, 32, 128), (1024, 4096, 8192),
+                                                      (0.25, 0.75, 0.99), (1, 2, 3)):
+        yield (dict(requests=requests, context=context, fraction=fraction, depth=depth),
+               grid_tree(requests, context, fraction, depth))
+
+
+def calibration_grid():
+    """Yield ``(name, spec)`` of cost-model calibration shapes (disjoint lengths and counts)."""
+    for requests in (6, 20, 40, 96):
+        for root, private in ((600, 40), (1500, 100), (3000, 300), (5000, 20)):
+            yield f"shared_r{requests}_{root}_{private}", shared_prefix(requests, root, private)
+    for requests in (6, 20, 40):
+        for private in (700, 2000):
+            yield f"private_r{requests}_{private}", shared_prefix(requests, 0, private)
