@@ -22,6 +22,9 @@ FLAGS = [
     "-mcode-object-version=5",
     # packed-FP32 VALU forms are kept out of every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: every kernel fits in 256 VGPRs, and the
+    # AGPR form made the allocator copy O between register files each step
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function",
 ]
 

@@ -47,7 +47,6 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int TT = 64;          // tokens per staged tile
 constexpr int NT = 256;         // threads per workgroup (4 waves)
 constexpr float LN2 = 0.69314718055994530942f;
 constexpr float NEG_INF = -__builtin_inff();
@@ -109,27 +108,40 @@ struct SegParams {
     float scale_log2;  // log2(e) / sqrt(D)
 };
 
+// Lazy rescaling threshold in log2 units: a row's running maximum is only
+// raised when a score exceeds it by more than TAU, so exponentials stay
+// <= 2^TAU and the accumulator rescale (a pass over all of O) is skipped on
+// almost every step.  The final log-sum-exp is exact for any stale maximum.
+constexpr float TAU = 8.0f;
+
 // ------------------------------------------------------- tile staging (LDS)
-// One 64-token tile of one KV head: Kt[TT][D] (+pad) and Vt[D][TT] (+pad).
-template <int D>
+// One TTILE-token tile of one KV head: Kt[TTILE][D] (+pad) and Vt[D][TTILE]
+// (+pad), built from 8x8 element blocks that NTHR threads load with 16-byte
+// global loads, transpose in registers and store with 16-byte LDS writes.
+template <int D, int TTILE, int NTHR>
 struct Stage {
-    static constexpr int KS = D + 8;   // Kt row stride (elements); +16 B breaks bank aliasing
-    static constexpr int VS = TT + 8;  // Vt row stride
-    static constexpr int KELEMS = TT * KS;
+    // Row strides (elements).  Kt rows are read 16 B per lane, 8 lanes per LDS
+    // cycle: D + 8 shifts consecutive rows by 4 banks.  Vt rows are read 8 B per
+    // lane, 16 lanes per cycle: TTILE + 4 shifts consecutive rows by 2 banks, so
+    // 16 rows cover all 32 banks once.
+    static constexpr int KS = D + 8;
+    static constexpr int VS = TTILE + 4;
+    static constexpr int KELEMS = TTILE * KS;
     static constexpr int ELEMS = KELEMS + D * VS;
     static constexpr int DG = D / 8;
-    static constexpr int TG = TT / 8;
+    static constexpr int TG = TTILE / 8;
     static constexpr int KBLK = DG * TG;  // 8x8 blocks per operand
-    static constexpr int VBLK = TG * DG;
+    static constexpr int NBLK = 2 * KBLK;
+    static constexpr int BPT = (NBLK + NTHR - 1) / NTHR;  // blocks per thread
 
-    u32x4 r[8];
+    u32x4 r[BPT][8];
 
     __device__ static u32x4 load_tail(const u16 *p, int valid) {
         u32 w[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            u32 lo = (2 * k < valid) ? (u32)p[2 * k] : 0u;
-            u32 hi = (2 * k + 1 < valid) ? (u32)p[2 * k + 1] : 0u;
+            const u32 lo = (2 * k < valid) ? (u32)p[2 * k] : 0u;
+            const u32 hi = (2 * k + 1 < valid) ? (u32)p[2 * k + 1] : 0u;
             w[k] = lo | (hi << 16);
         }
         return u32x4{w[0], w[1], w[2], w[3]};
@@ -137,57 +149,89 @@ struct Stage {
 
     // Global -> registers.  Tokens [t0, t0 + nvalid) are read; the rest of the
     // tile is zero (zero V keeps masked columns finite in PV).
-    __device__ void load(const u16 *__restrict__ kp, const u16 *__restrict__ vp, int h, int tcap,
-                         int t0, int nvalid, bool kaligned, int tid) {
-        if (tid < KBLK) {
-            const int dg = tid % DG, tg = tid / DG;
-            const u16 *base = kp + ((size_t)(h * D + 8 * dg) * tcap + t0 + 8 * tg);
-            const int valid = nvalid - 8 * tg;
-            if (kaligned && valid >= 8) {
+    __device__ void load(const u16 *__restrict__ kp, const u16 *__restrict__ vp, int h, int tcap, int t0,
+                         int nvalid, bool kaligned, int tid) {
+        if (kaligned && nvalid >= TTILE) {
+            // full, 16-byte aligned tile: unconditional vector loads (wave-uniform branch)
 #pragma unroll
-                for (int i = 0; i < 8; ++i) r[i] = *(const u32x4 *)(base + (size_t)i * tcap);
-            } else {
+            for (int j = 0; j < BPT; ++j) {
+                const int b = tid + j * NTHR;
+                if (b < KBLK) {
+                    const int dg = b % DG, tg = b / DG;
+                    const u16 *base = kp + ((size_t)(h * D + 8 * dg) * tcap + t0 + 8 * tg);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) r[i] = load_tail(base + (size_t)i * tcap, valid);
+                    for (int i = 0; i < 8; ++i) r[j][i] = *(const u32x4 *)(base + (size_t)i * tcap);
+                } else if (b < NBLK) {
+                    const int u = b - KBLK;
+                    const int tg = u % TG, dg = u / TG;
+                    const u16 *base = vp + ((size_t)(h * tcap + t0 + 8 * tg) * D + 8 * dg);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) r[j][i] = *(const u32x4 *)(base + i * D);
+                }
             }
-        } else if (tid < KBLK + VBLK) {
-            const int u = tid - KBLK;
-            const int tg = u % TG, dg = u / TG;
-            const u16 *base = vp + ((size_t)(h * tcap + t0 + 8 * tg) * D + 8 * dg);
+            return;
+        }
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                r[i] = (8 * tg + i < nvalid) ? *(const u32x4 *)(base + (size_t)i * D) : u32x4{0, 0, 0, 0};
+        for (int j = 0; j < BPT; ++j) {
+            const int b = tid + j * NTHR;
+            if (b < KBLK) {
+                const int dg = b % DG, tg = b / DG;
+                const u16 *base = kp + ((size_t)(h * D + 8 * dg) * tcap + t0 + 8 * tg);
+                const int valid = nvalid - 8 * tg;
+                if (kaligned && valid >= 8) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) r[j][i] = *(const u32x4 *)(base + (size_t)i * tcap);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) r[j][i] = load_tail(base + (size_t)i * tcap, valid);
+                }
+            } else if (b < NBLK) {
+                const int u = b - KBLK;
+                const int tg = u % TG, dg = u / TG;
+                const u16 *base = vp + ((size_t)(h * tcap + t0 + 8 * tg) * D + 8 * dg);
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    r[j][i] = (8 * tg + i < nvalid) ? *(const u32x4 *)(base + (size_t)i * D) : u32x4{0, 0, 0, 0};
+            }
         }
     }
 
-    // 8x8 transpose of 16-bit elements: out[j] = column j of the rows in r.
-    __device__ void transpose(u32x4 (&o)[8]) const {
+    // 8x8 transpose of 16-bit elements: o[c] = column c of the rows in in[].
+    __device__ static void transpose(const u32x4 (&in)[8], u32x4 (&o)[8]) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int c = 0; c < 8; ++c) {
             u32 w[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const u32 a = r[2 * k][j >> 1], b = r[2 * k + 1][j >> 1];
-                w[k] = (j & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+                const u32 a = in[2 * k][c >> 1], b = in[2 * k + 1][c >> 1];
+                w[k] = (c & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
             }
-            o[j] = u32x4{w[0], w[1], w[2], w[3]};
+            o[c] = u32x4{w[0], w[1], w[2], w[3]};
         }
     }
 
     // Registers -> LDS in MFMA operand order.
     __device__ void store(u16 *lds, int tid) const {
-        if (tid >= KBLK + VBLK) return;
-        u32x4 o[8];
-        transpose(o);
-        if (tid < KBLK) {
-            const int dg = tid % DG, tg = tid / DG;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) *(u32x4 *)(lds + (8 * tg + j) * KS + 8 * dg) = o[j];
-        } else {
-            const int u = tid - KBLK;
-            const int tg = u % TG, dg = u / TG;
+        for (int j = 0; j < BPT; ++j) {
+            const int b = tid + j * NTHR;
+            if (b >= NBLK) continue;
+            u32x4 o[8];
+            transpose(r[j], o);
+            if (b < KBLK) {
+                const int dg = b % DG, tg = b / DG;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) *(u32x4 *)(lds + KELEMS + (8 * dg + j) * VS + 8 * tg) = o[j];
+                for (int c = 0; c < 8; ++c) *(u32x4 *)(lds + (8 * tg + c) * KS + 8 * dg) = o[c];
+            } else {
+                const int u = b - KBLK;
+                const int tg = u % TG, dg = u / TG;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    u16 *dst = lds + KELEMS + (8 * dg + c) * VS + 8 * tg;  // 8-byte aligned
+                    *(u32x2 *)dst = u32x2{o[c][0], o[c][1]};
+                    *(u32x2 *)(dst + 4) = u32x2{o[c][2], o[c][3]};
+                }
+            }
         }
     }
 };
@@ -208,121 +252,203 @@ __device__ inline void load_q(const SegParams &p, int job, int h, int row, int n
     }
 }
 
-// --------------------------------------------------------- small segments
-// One workgroup per (job, KV head) with at most 16 query rows.
-template <int D, bool FP16>
-__global__ __launch_bounds__(NT) void seg_small_kernel(SegParams p) {
-    using S = Stage<D>;
+// Online-softmax state of NB 16-row blocks held by one wave.  Lane (row, g4)
+// keeps the shared (stale) maximum m of its row, a partial denominator z over
+// its own columns and O^T[d = 16*db + 4*g4 + i][row] in o[nb][db][i].
+template <int D, int NB>
+struct RowState {
+    float m[NB], z[NB];
+    f32x4 o[NB][D / 16];
+
+    __device__ void reset() {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            m[nb] = NEG_INF;
+            z[nb] = 0.f;
+#pragma unroll
+            for (int db = 0; db < D / 16; ++db) o[nb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+};
+
+// S^T = K Q^T for one 32-token step: s[nb][b][i] is the score of token
+// 16*b + 4*g4 + i (relative to kt) against row 16*nb + row.
+template <int D, bool FP16, int NB, int KS>
+__device__ inline void qk_step(const u16 *kt, int row, int g4, const u32x4 (&qf)[NB][D / 32], f32x4 (&s)[NB][2]) {
     using O = Ops<FP16>;
-    __shared__ __attribute__((aligned(16))) u16 lds[S::ELEMS];
-
-    const int job = p.items[blockIdx.x];
-    const int h = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row = lane & 15, g4 = lane >> 4;
-    const int kst = p.kstart[job];
-    const int ntok = max(0, min(p.klen[job], p.tcap - kst));
-    const int nrows = min(p.qlen[job] * p.group, 16);
-    const bool kal = ((p.tcap | kst) & 7) == 0;
-    const float c = p.scale_log2;
-
-    u32x4 qf[D / 32];
-    load_q<D>(p, job, h, row, nrows, g4, qf);
-
-    float m = NEG_INF, z = 0.f;
-    f32x4 o[D / 16];
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const int ntiles = (ntok + TT - 1) / TT;
-    S st;
-    if (ntiles > 0) st.load(p.kp, p.vp, h, p.tcap, kst, min(ntok, TT), kal, tid);
-    const int base = 16 * wave;
-    for (int it = 0; it < ntiles; ++it) {
-        __syncthreads();
-        st.store(lds, tid);
-        __syncthreads();
-        const int t0 = it * TT;
-        const int nv = ntok - t0;
-        if (it + 1 < ntiles) st.load(p.kp, p.vp, h, p.tcap, kst + t0 + TT, min(nv - TT, TT), kal, tid);
-        if (base < nv) {
-            f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < NB; ++nb) s[nb][0] = s[nb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) {
-                const u32x4 a = *(const u32x4 *)(lds + (base + row) * S::KS + 32 * ks + 8 * g4);
-                s = O::mma_k32(a, qf[ks], s);
-            }
-            // s[i] <-> token base + 4*g4 + i of query row `row`
-            float sv[4];
-            float mx = NEG_INF;
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const u32x4 a = *(const u32x4 *)(kt + (16 * b + row) * KS + 32 * ks + 8 * g4);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) s[nb][b] = O::mma_k32(a, qf[nb][ks], s[nb][b]);
+        }
+    }
+}
+
+// Softmax update and O^T += V^T P^T for one 32-token step with nvs valid
+// tokens.  PV k-slot j of lane group g4 is token 4*g4 + j (j < 4) or
+// 16 + 4*g4 + j - 4 (j >= 4), which is where the QK output left P.
+template <int D, bool FP16, int NB, int VS>
+__device__ inline void pv_step(const u16 *vt, int row, int g4, f32x4 (&s)[NB][2], int nvs, float c,
+                               RowState<D, NB> &st) {
+    using O = Ops<FP16>;
+    u32x4 vf[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+        const u16 *vr = vt + (16 * db + row) * VS + 4 * g4;
+        const u32x2 lo = *(const u32x2 *)vr;
+        const u32x2 hi = *(const u32x2 *)(vr + 16);
+        vf[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+    const bool full = nvs >= 32;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        float x[8];
+        float lm = NEG_INF;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                sv[i] = (base + 4 * g4 + i < nv) ? s[i] : NEG_INF;
-                mx = fmaxf(mx, sv[i]);
+                float v = s[nb][b][i];
+                if (!full && 16 * b + 4 * g4 + i >= nvs) v = NEG_INF;
+                x[4 * b + i] = v;
+                lm = fmaxf(lm, v);
             }
-            mx = xor_max(mx);
-            const float mn = fmaxf(m, mx * c);
-            const float alpha = fast_exp2(m - mn);
-            float pr[4];
+        const bool need = lm * c > st.m[nb] + TAU;
+        if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform, rare after the first step
+            const float mn = fmaxf(st.m[nb], xor_max(lm) * c);
+            const float alpha = fast_exp2(st.m[nb] - mn);
+            st.z[nb] *= alpha;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(sv[i] * c - mn);
-            z = z * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-            m = mn;
-            const u32x2 pb = {O::pack(pr[0], pr[1]), O::pack(pr[2], pr[3])};
-#pragma unroll
-            for (int db = 0; db < D / 16; ++db) {
-                const u32x2 a = *(const u32x2 *)(lds + S::KELEMS + (16 * db + row) * S::VS + base + 4 * g4);
-                o[db] = O::mma_k16(a, pb, o[db] * alpha);
-            }
+            for (int db = 0; db < D / 16; ++db) st.o[nb][db] *= alpha;
+            st.m[nb] = mn;
         }
+        float pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(__builtin_fmaf(x[i], c, -st.m[nb]));
+        st.z[nb] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+        const u32x4 pb = {O::pack(pr[0], pr[1]), O::pack(pr[2], pr[3]), O::pack(pr[4], pr[5]),
+                          O::pack(pr[6], pr[7])};
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) st.o[nb][db] = O::mma_k32(vf[db], pb, st.o[nb][db]);
     }
+}
 
-    // Combine the four waves' (m, z, O) through LDS.
-    const float zr = xor_sum(z);
-    __syncthreads();
-    float *red = reinterpret_cast<float *>(lds);  // [4 waves][16 rows][D]
-    float *mz = red + 4 * 16 * D;                 // [2][4 waves][16 rows]
-    static_assert(sizeof(u16) * S::ELEMS >= sizeof(float) * (4 * 16 * D + 128), "LDS reuse");
-    if (g4 == 0) {
-        mz[wave * 16 + row] = m;
-        mz[64 + wave * 16 + row] = zr;
-    }
-#pragma unroll
-    for (int db = 0; db < D / 16; ++db) *(f32x4 *)(red + (wave * 16 + row) * D + 16 * db + 4 * g4) = o[db];
-    __syncthreads();
+// Normalise and store the partial rows of NB 16-row blocks (rows >= nrows skipped).
+template <int D, int NB>
+__device__ inline void store_rows(const SegParams &p, RowState<D, NB> &st, int job, int h, int wrow0, int nrows,
+                                  int row, int g4) {
     const int rb = p.rowbase[job];
-    for (int cidx = tid; cidx < 16 * (D / 4); cidx += NT) {
-        const int r = cidx / (D / 4), d4 = cidx - r * (D / 4);
-        if (r >= nrows) continue;
-        const int lr = r / p.group, gg = r - lr * p.group;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const float zr = xor_sum(st.z[nb]);
+        const int grow = wrow0 + 16 * nb + row;
+        if (grow >= nrows) continue;
+        const int lr = grow / p.group, gg = grow - lr * p.group;
         const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
-        float M = NEG_INF;
+        float *dst = p.part + prow * D + 4 * g4;
+        const bool any = st.m[nb] != NEG_INF;
+        const float inv = any ? 1.f / zr : 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, mz[w * 16 + r]);
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        float Z = 0.f;
-        if (M != NEG_INF) {
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const float sc = fast_exp2(mz[w * 16 + r] - M);
-                Z += mz[64 + w * 16 + r] * sc;
-                acc += sc * *(const f32x4 *)(red + (w * 16 + r) * D + 4 * d4);
+        for (int db = 0; db < D / 16; ++db) *(f32x4 *)(dst + 16 * db) = st.o[nb][db] * inv;
+        if (g4 == 0) p.lse[prow] = any ? (st.m[nb] + __builtin_amdgcn_logf(zr)) * LN2 : NEG_INF;
+    }
+}
+
+// --------------------------------------------------------- small segments
+// Jobs with at most 16 query rows (e.g. one request's private tail).  One
+// wave per workgroup walks a strided list of (job, KV head) items; 32-token
+// tiles go through wave-private LDS and the next tile -- of the same item or
+// of the next one -- is already in flight while the current one is computed.
+constexpr int SMALL_TT = 32;
+constexpr int SMALL_NT = 64;
+
+template <int D, bool FP16>
+__global__ __launch_bounds__(SMALL_NT) void seg_small_kernel(SegParams p) {
+    using S = Stage<D, SMALL_TT, SMALL_NT>;
+    __shared__ __attribute__((aligned(16))) u16 lds[S::ELEMS];
+    const int lane = threadIdx.x;
+    const int row = lane & 15, g4 = lane >> 4;
+    const int total = p.n_items * p.hk;
+    const float c = p.scale_log2;
+    const int stride = gridDim.x;
+
+    struct Item {
+        int job, h, kst, ntok, ntiles;
+        bool kal;
+    };
+    auto decode = [&](int idx) {
+        Item it;
+        it.job = p.items[idx / p.hk];
+        it.h = idx - (idx / p.hk) * p.hk;
+        it.kst = p.kstart[it.job];
+        it.ntok = max(0, min(p.klen[it.job], p.tcap - it.kst));
+        it.ntiles = (it.ntok + SMALL_TT - 1) / SMALL_TT;
+        it.kal = ((p.tcap | it.kst) & 7) == 0;
+        return it;
+    };
+
+    S st;
+    // prefetch cursor: (pidx, ptile) is the tile whose loads sit in st.r
+    int pidx = blockIdx.x, ptile = 0;
+    Item pit;
+    while (pidx < total) {
+        pit = decode(pidx);
+        if (pit.ntiles > 0) break;
+        pidx += stride;
+    }
+    if (pidx < total)
+        st.load(p.kp, p.vp, pit.h, p.tcap, pit.kst, min(pit.ntok, SMALL_TT), pit.kal, lane);
+
+    RowState<D, 1> rs;
+    u32x4 qf[1][D / 32];
+    for (int idx = blockIdx.x; idx < total; idx += stride) {
+        const Item it = decode(idx);
+        const int nrows = min(p.qlen[it.job] * p.group, 16);
+        load_q<D>(p, it.job, it.h, row, nrows, g4, qf[0]);
+        rs.reset();
+        for (int t = 0; t < it.ntiles; ++t) {
+            __syncthreads();
+            st.store(lds, lane);
+            __syncthreads();
+            // advance the prefetch cursor and issue the next tile's loads
+            if (++ptile >= pit.ntiles) {
+                ptile = 0;
+                for (pidx += stride; pidx < total; pidx += stride) {
+                    pit = decode(pidx);
+                    if (pit.ntiles > 0) break;
+                }
             }
-            acc *= 1.f / Z;
+            if (pidx < total) {
+                const int t0 = ptile * SMALL_TT;
+                st.load(p.kp, p.vp, pit.h, p.tcap, pit.kst + t0, min(pit.ntok - t0, SMALL_TT), pit.kal, lane);
+            }
+            f32x4 s[1][2];
+            qk_step<D, FP16, 1, S::KS>(lds, row, g4, qf, s);
+            pv_step<D, FP16, 1, S::VS>(lds + S::KELEMS, row, g4, s, it.ntok - t * SMALL_TT, c, rs);
         }
-        *(f32x4 *)(p.part + prow * D + 4 * d4) = acc;
-        if (d4 == 0) p.lse[prow] = (M != NEG_INF) ? (M + __builtin_amdgcn_logf(Z)) * LN2 : NEG_INF;
+        store_rows<D, 1>(p, rs, it.job, it.h, 0, nrows, row, g4);
     }
 }
 
 // --------------------------------------------------------- large segments
-// One workgroup per (job, row tile of 64*NB rows, KV head); wave w owns rows
-// [16*NB*w, 16*NB*(w+1)) of the tile.
-template <int D, bool FP16, int NB>
-__global__ __launch_bounds__(NT) void seg_large_kernel(SegParams p) {
-    using S = Stage<D>;
-    using O = Ops<FP16>;
-    __shared__ __attribute__((aligned(16))) u16 lds[S::ELEMS];
+// One workgroup (NW waves) per (job, row tile of 16*NB*NW rows, KV head);
+// wave w owns rows [16*NB*w, 16*NB*(w+1)) of the tile.  TT-token K/V tiles
+// are double-buffered in LDS (one barrier per tile) and every K/V fragment
+// read from LDS feeds NB MFMAs.  Within a tile the next 32-token step's QK is
+// issued before the current step's softmax so the matrix cores and the VALU
+// have independent work; with 32 rows per wave everything stays in VGPRs and
+// two waves share each SIMD.
+template <int D, bool FP16, int NB, int NW, int TT>
+__global__ __launch_bounds__(64 * NW) void seg_large_kernel(SegParams p) {
+    constexpr int NTHR = 64 * NW;
+    constexpr int STEPS = TT / 32;
+    using S = Stage<D, TT, NTHR>;
+    __shared__ __attribute__((aligned(16))) u16 lds[2 * S::ELEMS];
 
     // Linear block L runs on XCD L % 8; give every XCD a contiguous range of
     // items so neighbouring row tiles of one (job, head) share an L2.
@@ -345,148 +471,151 @@ __global__ __launch_bounds__(NT) void seg_large_kernel(SegParams p) {
     u32x4 qf[NB][D / 32];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) load_q<D>(p, job, h, wrow0 + 16 * nb + row, nrows, g4, qf[nb]);
-
-    float m[NB], z[NB];
-    f32x4 o[NB][D / 16];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        m[nb] = NEG_INF;
-        z[nb] = 0.f;
-#pragma unroll
-        for (int db = 0; db < D / 16; ++db) o[nb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    RowState<D, NB> rs;
+    rs.reset();
 
     const int ntiles = (ntok + TT - 1) / TT;
     S st;
-    if (ntiles > 0) st.load(p.kp, p.vp, h, p.tcap, kst, min(ntok, TT), kal, tid);
-    for (int it = 0; it < ntiles; ++it) {
-        __syncthreads();
+    if (ntiles > 0) {
+        st.load(p.kp, p.vp, h, p.tcap, kst, min(ntok, TT), kal, tid);
         st.store(lds, tid);
-        __syncthreads();
-        const int t0 = it * TT;
-        const int nv = ntok - t0;
-        if (it + 1 < ntiles) st.load(p.kp, p.vp, h, p.tcap, kst + t0 + TT, min(nv - TT, TT), kal, tid);
-        if (!active) continue;
+    }
+    if (ntiles > 1) st.load(p.kp, p.vp, h, p.tcap, kst + TT, min(ntok - TT, TT), kal, tid);
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {
+        const u16 *cur = lds + (it & 1) * S::ELEMS;
+        const int nv = ntok - it * TT;
+        if (active) {
+            f32x4 sc[2][NB][2];
+            qk_step<D, FP16, NB, S::KS>(cur, row, g4, qf, sc[0]);
 #pragma unroll
-        for (int hh = 0; hh < TT / 32; ++hh) {
-            const int base = 32 * hh;
-            if (base >= nv) break;
-            f32x4 s[NB][2];
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) s[nb][0] = s[nb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-#pragma unroll
-                for (int ks = 0; ks < D / 32; ++ks) {
-                    const u32x4 a = *(const u32x4 *)(lds + (base + 16 * b + row) * S::KS + 32 * ks + 8 * g4);
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb) s[nb][b] = O::mma_k32(a, qf[nb][ks], s[nb][b]);
-                }
-            }
-            // V^T fragments; k-slot j <-> token base + 4*g4 + j (j < 4), base + 16 + 4*g4 + j - 4 (j >= 4)
-            u32x4 vf[D / 16];
-#pragma unroll
-            for (int db = 0; db < D / 16; ++db) {
-                const u16 *vr = lds + S::KELEMS + (16 * db + row) * S::VS + base + 4 * g4;
-                const u32x2 lo = *(const u32x2 *)vr;
-                const u32x2 hi = *(const u32x2 *)(vr + 16);
-                vf[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-            }
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                float sv[8];
-                float mx = NEG_INF;
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float x = (base + 16 * b + 4 * g4 + i < nv) ? s[nb][b][i] : NEG_INF;
-                        sv[4 * b + i] = x;
-                        mx = fmaxf(mx, x);
-                    }
-                mx = xor_max(mx);
-                const float mn = fmaxf(m[nb], mx * c);
-                const float alpha = fast_exp2(m[nb] - mn);
-                float pr[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(sv[i] * c - mn);
-                z[nb] = z[nb] * alpha + (((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7])));
-                m[nb] = mn;
-                const u32x4 pb = {O::pack(pr[0], pr[1]), O::pack(pr[2], pr[3]), O::pack(pr[4], pr[5]),
-                                  O::pack(pr[6], pr[7])};
-#pragma unroll
-                for (int db = 0; db < D / 16; ++db) o[nb][db] = O::mma_k32(vf[db], pb, o[nb][db] * alpha);
+            for (int k = 0; k < STEPS; ++k) {
+                const int base = 32 * k;
+                if (base >= nv) break;
+                if (k + 1 < STEPS && base + 32 < nv)
+                    qk_step<D, FP16, NB, S::KS>(cur + (base + 32) * S::KS, row, g4, qf, sc[(k + 1) & 1]);
+                pv_step<D, FP16, NB, S::VS>(cur + S::KELEMS + base, row, g4, sc[k & 1], nv - base, c, rs);
             }
         }
+        if (it + 1 < ntiles) st.store(lds + ((it + 1) & 1) * S::ELEMS, tid);
+        __syncthreads();
+        if (it + 2 < ntiles) {
+            const int t0 = (it + 2) * TT;
+            st.load(p.kp, p.vp, h, p.tcap, kst + t0, min(ntok - t0, TT), kal, tid);
+        }
     }
-
-    if (!active) return;
-    const int rb = p.rowbase[job];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        const float zr = xor_sum(z[nb]);
-        const int grow = wrow0 + 16 * nb + row;
-        if (grow >= nrows) continue;
-        const int lr = grow / p.group, gg = grow - lr * p.group;
-        const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
-        float *dst = p.part + prow * D + 4 * g4;
-        const bool any = m[nb] != NEG_INF;
-        const float inv = any ? 1.f / zr : 0.f;
-#pragma unroll
-        for (int db = 0; db < D / 16; ++db) *(f32x4 *)(dst + 16 * db) = o[nb][db] * inv;
-        if (g4 == 0) p.lse[prow] = any ? (m[nb] + __builtin_amdgcn_logf(zr)) * LN2 : NEG_INF;
-    }
+    if (active) store_rows<D, NB>(p, rs, job, h, wrow0, nrows, row, g4);
 }
 
 // ------------------------------------------------------------------ merge
-// One thread per (request, query head, 4 head-dim elements).
+// One workgroup per (request, group of MH query heads): the MH*D partial
+// elements of one slot are contiguous, so every slot is one coalesced
+// 16-byte-per-thread sweep.  The request's slot list, the log-sum-exp values
+// and the normalised merge weights are staged in LDS first; the slot loop is
+// unrolled so several slots' loads are in flight per thread.
+constexpr int MERGE_MAX_SLOTS = 256;
+
 template <int D, bool FP16>
 __global__ __launch_bounds__(NT) void merge_kernel(const float *__restrict__ part, const float *__restrict__ lse,
                                                    const int32_t *__restrict__ slots,
                                                    const int32_t *__restrict__ counts, u16 *__restrict__ out,
                                                    int hq, int maxs) {
-    constexpr int TPH = D / 4;  // threads per head
-    constexpr int HPB = NT / TPH;
+    constexpr int TPH = D / 4;    // threads per head
+    constexpr int MH = NT / TPH;  // heads per workgroup
+    __shared__ int sl[MERGE_MAX_SLOTS];
+    __shared__ float w[MERGE_MAX_SLOTS * MH];
+    __shared__ float mh[MH], invz[MH];
+
     const int r = blockIdx.x;
-    const int head = blockIdx.y * HPB + threadIdx.x / TPH;
-    const int d4 = threadIdx.x % TPH;
-    if (head >= hq) return;
+    const int h0 = blockIdx.y * MH;
+    const int nh = min(MH, hq - h0);
+    const int tid = threadIdx.x;
     const int cnt = counts[r];
-    const int32_t *sl = slots + (size_t)r * maxs;
-    float M = NEG_INF;
-    for (int s = 0; s < cnt; ++s) M = fmaxf(M, lse[(size_t)sl[s] * hq + head]);
+    const int32_t *slr = slots + (size_t)r * maxs;
+    const int hl = tid / TPH, d4 = tid % TPH;
+    const int head = h0 + hl;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (M != NEG_INF) {
-        float Z = 0.f;
-        for (int s = 0; s < cnt; ++s) {
-            const size_t prow = (size_t)sl[s] * hq + head;
-            const float w = fast_exp2((lse[prow] - M) * 1.44269504088896341f);
-            Z += w;
-            acc += w * *(const f32x4 *)(part + prow * D + 4 * d4);
+
+    if (cnt <= MERGE_MAX_SLOTS) {
+        for (int i = tid; i < cnt; i += NT) sl[i] = slr[i];
+        __syncthreads();
+        for (int i = tid; i < cnt * MH; i += NT) {
+            const int s = i / MH, j = i - s * MH;
+            w[i] = j < nh ? lse[(size_t)sl[s] * hq + h0 + j] : NEG_INF;
         }
-        acc *= 1.f / Z;
+        __syncthreads();
+        if (tid < MH) {
+            float M = NEG_INF;
+            for (int s = 0; s < cnt; ++s) M = fmaxf(M, w[s * MH + tid]);
+            float Z = 0.f;
+            if (M != NEG_INF)
+                for (int s = 0; s < cnt; ++s) Z += fast_exp2((w[s * MH + tid] - M) * 1.44269504088896341f);
+            mh[tid] = M;
+            invz[tid] = Z > 0.f ? 1.f / Z : 0.f;
+        }
+        __syncthreads();
+        for (int i = tid; i < cnt * MH; i += NT) {
+            const int j = i % MH;
+            w[i] = mh[j] != NEG_INF ? fast_exp2((w[i] - mh[j]) * 1.44269504088896341f) * invz[j] : 0.f;
+        }
+        __syncthreads();
+        if (hl < nh) {
+            const float *src = part + (size_t)head * D + 4 * d4;
+            const size_t srow = (size_t)hq * D;
+            int s = 0;
+            for (; s + 8 <= cnt; s += 8) {
+                f32x4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = *(const f32x4 *)(src + sl[s + u] * srow);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc += w[(s + u) * MH + hl] * v[u];
+            }
+            for (; s < cnt; ++s) acc += w[s * MH + hl] * *(const f32x4 *)(src + sl[s] * srow);
+        }
+    } else if (hl < nh) {
+        // many slots: two passes straight from global memory
+        float M = NEG_INF;
+        for (int s = 0; s < cnt; ++s) M = fmaxf(M, lse[(size_t)slr[s] * hq + head]);
+        if (M != NEG_INF) {
+            float Z = 0.f;
+            for (int s = 0; s < cnt; ++s) {
+                const size_t prow = (size_t)slr[s] * hq + head;
+                const float wt = fast_exp2((lse[prow] - M) * 1.44269504088896341f);
+                Z += wt;
+                acc += wt * *(const f32x4 *)(part + prow * D + 4 * d4);
+            }
+            acc *= 1.f / Z;
+        }
     }
-    u16 *dst = out + ((size_t)r * hq + head) * D + 4 * d4;
-    const u32x2 packed = {Ops<FP16>::pack(acc[0], acc[1]), Ops<FP16>::pack(acc[2], acc[3])};
-    *(u32x2 *)dst = packed;
+    if (hl < nh) {
+        u16 *dst = out + ((size_t)r * hq + head) * D + 4 * d4;
+        const u32x2 packed = {Ops<FP16>::pack(acc[0], acc[1]), Ops<FP16>::pack(acc[2], acc[3])};
+        *(u32x2 *)dst = packed;
+    }
 }
 
 // ------------------------------------------------------------------ launch
+// resident one-wave workgroups on 256 CUs (8 per CU by LDS at d = 128)
+constexpr int SMALL_MAX_BLOCKS = 2048;
+
 template <int D, bool FP16>
 hipError_t launch_segment(const SegParams &sp, int kind, hipStream_t stream) {
     if (sp.n_items <= 0) return hipSuccess;
     switch (kind) {
-        case TA_SMALL:
-            hipLaunchKernelGGL((seg_small_kernel<D, FP16>), dim3(sp.n_items, sp.hk), dim3(NT), 0, stream, sp);
+        case TA_SMALL: {
+            const long total = (long)sp.n_items * sp.hk;
+            const int blocks = (int)(total < SMALL_MAX_BLOCKS ? total : SMALL_MAX_BLOCKS);
+            hipLaunchKernelGGL((seg_small_kernel<D, FP16>), dim3(blocks), dim3(SMALL_NT), 0, stream, sp);
             break;
+        }
         case TA_LARGE64:
-            hipLaunchKernelGGL((seg_large_kernel<D, FP16, 1>), dim3(sp.n_items), dim3(NT), 0, stream, sp);
+            hipLaunchKernelGGL((seg_large_kernel<D, FP16, 1, 4, 64>), dim3(sp.n_items), dim3(256), 0, stream, sp);
             break;
         case TA_LARGE128:
-            hipLaunchKernelGGL((seg_large_kernel<D, FP16, 2>), dim3(sp.n_items), dim3(NT), 0, stream, sp);
+            hipLaunchKernelGGL((seg_large_kernel<D, FP16, 2, 4, 64>), dim3(sp.n_items), dim3(256), 0, stream, sp);
             break;
         case TA_LARGE256:
-            hipLaunchKernelGGL((seg_large_kernel<D, FP16, 4>), dim3(sp.n_items), dim3(NT), 0, stream, sp);
+            hipLaunchKernelGGL((seg_large_kernel<D, FP16, 2, 8, 128>), dim3(sp.n_items), dim3(512), 0, stream, sp);
             break;
         default:
             return (hipError_t)TA_ERR_ARG;
@@ -497,8 +626,8 @@ hipError_t launch_segment(const SegParams &sp, int kind, hipStream_t stream) {
 template <int D, bool FP16>
 hipError_t launch_merge(const float *part, const float *lse, const int32_t *slots, const int32_t *counts,
                         void *out, int nreq, int hq, int maxs, hipStream_t stream) {
-    constexpr int HPB = NT / (D / 4);
-    hipLaunchKernelGGL((merge_kernel<D, FP16>), dim3(nreq, (hq + HPB - 1) / HPB), dim3(NT), 0, stream, part,
+    constexpr int MH = NT / (D / 4);
+    hipLaunchKernelGGL((merge_kernel<D, FP16>), dim3(nreq, (hq + MH - 1) / MH), dim3(NT), 0, stream, part,
                        lse, slots, counts, static_cast<u16 *>(out), hq, maxs);
     return hipGetLastError();
 }

@@ -1,0 +1,80 @@
+"""Launch one kernel of a plan repeatedly for profiling (cf. scripts/profile_kernel.py in the reference).
+
+    python -m tree_attention.profile_kernel --shape wide_long --method cube \
+        --cost-model mi355x --kernel large256 --iters 20
+
+``--kernel`` is one of ``small``, ``large64``, ``large128``, ``large256``,
+``merge`` or ``layer`` (the whole attention_matrix call).  K/V rotate over
+``--pools`` copies so repeated launches read HBM, not the MALL.  Prints the
+mean device time per launch measured with HIP events.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+
+import torch
+
+from . import CostModel, schedule, shapes
+from . import _native
+from .kernels import attention_matrix, merge, pack_kv, prepare, segment
+
+KINDS = {"small": _native.TA_SMALL, "large64": _native.TA_LARGE64, "large128": _native.TA_LARGE128,
+         "large256": _native.TA_LARGE256}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--shape", default="wide_long")
+    ap.add_argument("--method", default="cube")
+    ap.add_argument("--cost-model", default="mi355x", choices=["mi355x", "reference"])
+    ap.add_argument("--kernel", default="layer", choices=sorted(KINDS) + ["merge", "layer"])
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--pools", type=int, default=8)
+    ap.add_argument("--heads", default="32,8,128")
+    ap.add_argument("--param", action="append", default=[],
+                    help="CostModel field override, e.g. --param kv_split=1024 (repeatable)")
+    args = ap.parse_args(argv)
+    hq, hk, d = map(int, args.heads.split(","))
+    spec = shapes.benchmark_cases()[args.shape]
+    tree = shapes.tree(spec)
+    model = CostModel.mi355x() if args.cost_model == "mi355x" else CostModel()
+    for kv in args.param:
+        key, val = kv.split("=")
+        setattr(model, key, type(getattr(model, key))(float(val)))
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(101)
+    q = torch.randn(len(tree.paths), hq, d, generator=g).bfloat16().to(dev)
+    k = torch.randn(tree.storage_tokens, hk, d, generator=g).bfloat16().to(dev)
+    v = torch.randn(tree.storage_tokens, hk, d, generator=g).bfloat16().to(dev)
+    kp, vp = pack_kv(k, v)
+    pools = [(kp, vp)] + [(kp.clone(), vp.clone()) for _ in range(args.pools - 1)]
+    prepared = prepare(schedule(tree, hq, hk, d, args.method, model), q)
+    attention_matrix(q, kp, vp, prepared)  # partials exist before a lone merge
+
+    def launch(i):
+        kpi, vpi = pools[i % len(pools)]
+        if args.kernel == "layer":
+            attention_matrix(q, kpi, vpi, prepared)
+        elif args.kernel == "merge":
+            merge(prepared)
+        else:
+            segment(q, kpi, vpi, prepared, KINDS[args.kernel])
+
+    for i in range(3):
+        launch(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.iters):
+        launch(i)
+    end.record()
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel": args.kernel, "shape": args.shape, "method": args.method,
+                      "params": {f: getattr(model, f) for f in ("kv_split", "max_query_rows")},
+                      "iters": args.iters, "us_per_launch": start.elapsed_time(end) * 1e3 / args.iters,
+                      "items": list(prepared.abi.n_items)}), flush=True)
+
+
+if __name__ == "__main__":
+    main()
