@@ -1,0 +1,181 @@
+"""Qwen3 decoding over shared per-layer KV pools (drop-in for the reference's ``qwen.py``).
+
+``SharedKVDecoder`` (reference src/tree_attention/qwen.py:9-103) and
+``CachedPrefixDecoder`` (:106-124) keep their constructor arguments, public
+attributes (``tree``, ``sequences``, ``pools``, ``logits``, ``used``,
+``prefix_size``, ``generated``, ``max_new_tokens``, ``capacity``) and
+``step(token_ids) -> logits``.
+
+Pool layout (the layout the HIP segment kernels read):
+
+* ``pools[layer] = (kp [HK, D, capacity], vp [HK, capacity, D])`` in the
+  model dtype; positions ``[0, prefix_size)`` hold the prompt tree in the
+  physical order fixed by ``KVTree.from_sequences``; request ``r``'s decode
+  tail occupies ``[prefix_size + r * max_new_tokens, prefix_size + (r + 1) *
+  max_new_tokens)`` (qwen.py:53-56), so every tail is one contiguous run.
+
+Per decode step each layer's attention forward is swapped for one that writes
+the step's RoPE'd K/V into the pools and calls ``attention_matrix`` on them;
+the original forwards are restored afterwards.  ``attention_matrix`` is looked
+up as this module's global at call time, so a checker may wrap it (the
+reference's scripts/model_checks.py:43,59 does).
+"""
+from __future__ import annotations
+
+from types import MethodType
+
+import torch
+
+from .kernels import CachedDecodePlan, attention_matrix, prepare
+from .schedule import CostModel, schedule
+from .tree import KVTree
+
+try:  # the model's own rotary helper (transformers >= 4.57)
+    from transformers.models.qwen3.modeling_qwen3 import apply_rotary_pos_emb
+except ImportError as exc:  # pragma: no cover - transformers is a hard dependency of this module
+    raise ImportError("tree_attention.qwen needs transformers with Qwen3 support") from exc
+
+
+def _find_leaf(tree: KVTree, request: int) -> int:
+    for i, node in enumerate(tree.nodes):
+        if request in node.terminal:
+            return i
+    raise ValueError(f"request {request} has no terminal node")
+
+
+class SharedKVDecoder:
+    """Greedy-decode driver whose attention reads one physical copy of shared prefixes.
+
+    ``sequences`` are token-id lists (one per request).  The prompt of every
+    request is prefilled with the model's own attention; afterwards every
+    ``step`` appends one token per request and re-plans the whole tree
+    (reference qwen.py:58-61,74-103).
+    """
+
+    def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None):
+        self.model = model
+        self.sequences = [list(s) for s in sequences]
+        self.tree = KVTree.from_sequences(self.sequences)
+        self.method = method
+        self.cost_model = cost_model or CostModel()
+        self.device = next(model.parameters()).device
+        cfg = model.config
+        self.hq = cfg.num_attention_heads
+        self.hk = cfg.num_key_value_heads
+        self.dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        self.original = [layer.self_attn.forward for layer in model.model.layers]
+        self.max_new_tokens = max_new_tokens
+        self.prefix_size = self.tree.storage_tokens
+        self.used = self.prefix_size
+        self.capacity = self.prefix_size + len(self.sequences) * max_new_tokens
+        self.generated = 0
+        dtype = model.dtype
+        self.pools = [(torch.empty((self.hk, self.dim, self.capacity), device=self.device, dtype=dtype),
+                       torch.empty((self.hk, self.capacity, self.dim), device=self.device, dtype=dtype))
+                      for _ in model.model.layers]
+        self.leaves = [_find_leaf(self.tree, r) for r in range(len(self.sequences))]
+        self._prefill()
+
+    # -------------------------------------------------------------- prefill
+    @torch.inference_mode()
+    def _prefill(self):
+        """Run each prompt once and scatter its not-yet-written K/V into the pools (qwen.py:34-51)."""
+        written = set()
+        last = []
+        for r, seq in enumerate(self.sequences):
+            out = self.model(torch.tensor([seq], device=self.device), use_cache=True)
+            last.append(out.logits[0, -1].clone())
+            path = self.tree.paths[r]
+            fresh = [i for i, pos in enumerate(path) if pos not in written]
+            if fresh:
+                src = torch.tensor(fresh, device=self.device)
+                dst = torch.tensor([path[i] for i in fresh], device=self.device)
+                for (kp, vp), layer in zip(self.pools, out.past_key_values.layers):
+                    # cache tensors are [batch, HK, positions, D]
+                    kp.index_copy_(2, dst, layer.keys[0].index_select(1, src).transpose(1, 2))
+                    vp.index_copy_(1, dst, layer.values[0].index_select(1, src))
+            written.update(path)
+        self.logits = torch.stack(last)
+
+    # ------------------------------------------------------------ decoding
+    def _next_positions(self, count):
+        """Pool slots of this step's tokens: one per request, in its reserved tail (qwen.py:53-56)."""
+        slots = [self.prefix_size + r * self.max_new_tokens + self.generated for r in range(count)]
+        self.generated += 1
+        return slots
+
+    def _prepare_plan(self):
+        plan = schedule(self.tree, self.hq, self.hk, self.dim, self.method, self.cost_model)
+        shape_of_q = torch.empty((len(self.sequences), self.hq, self.dim), device=self.device,
+                                 dtype=self.model.dtype)
+        return prepare(plan, shape_of_q)
+
+    def _append(self, token_ids):
+        if self.used + len(token_ids) > self.capacity:
+            raise ValueError("Decode exceeds allocated max_new_tokens")
+        slots = self._next_positions(len(token_ids))
+        for seq, tok in zip(self.sequences, token_ids):
+            seq.append(tok)
+        self.tree.extend_leaves(self.leaves, slots)
+        self.used += len(token_ids)
+        return slots
+
+    @torch.inference_mode()
+    def step(self, token_ids):
+        """Append one token per request and return next-token logits ``[R, vocab]`` (qwen.py:74-103)."""
+        token_ids = list(token_ids)
+        if len(token_ids) != len(self.sequences):
+            raise ValueError("step needs exactly one token per request")
+        rope_pos = torch.tensor([[len(s)] for s in self.sequences], device=self.device)
+        slots = torch.tensor(self._append(token_ids), device=self.device)
+        prepared = self._prepare_plan()
+        pools = self.pools
+        nreq = len(token_ids)
+
+        def forward(module, hidden_states, position_embeddings, attention_mask=None, **kwargs):
+            shape = (*hidden_states.shape[:-1], -1, module.head_dim)
+            q = module.q_norm(module.q_proj(hidden_states).view(shape)).transpose(1, 2)
+            k = module.k_norm(module.k_proj(hidden_states).view(shape)).transpose(1, 2)
+            v = module.v_proj(hidden_states).view(shape).transpose(1, 2)
+            q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
+            kp, vp = pools[module.layer_idx]
+            # q, k, v: [R, heads, 1, D] -> pool slots of this step
+            kp.index_copy_(2, slots, k[:, :, 0, :].permute(1, 2, 0))
+            vp.index_copy_(1, slots, v[:, :, 0, :].permute(1, 0, 2))
+            attn = attention_matrix(q[:, :, 0, :].contiguous(), kp, vp, prepared)
+            return module.o_proj(attn.reshape(nreq, 1, -1)), None
+
+        layers = self.model.model.layers
+        for layer in layers:
+            layer.self_attn.forward = MethodType(forward, layer.self_attn)
+        try:
+            out = self.model(torch.tensor(token_ids, device=self.device)[:, None], position_ids=rope_pos,
+                             use_cache=False)
+            self.logits = out.logits[:, 0]
+        finally:
+            for layer, original in zip(layers, self.original):
+                layer.self_attn.forward = original
+        return self.logits
+
+
+class CachedPrefixDecoder(SharedKVDecoder):
+    """Plans the prompt tree once; each step only sets the decode-tail lengths (qwen.py:106-124)."""
+
+    def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None):
+        super().__init__(model, sequences, max_new_tokens, method, cost_model)
+        prompt_plan = schedule(self.tree, self.hq, self.hk, self.dim, self.method, self.cost_model)
+        shape_of_q = torch.empty((len(self.sequences), self.hq, self.dim), device=self.device,
+                                 dtype=model.dtype)
+        self.cached_plan = CachedDecodePlan(prompt_plan, shape_of_q, self.prefix_size, max_new_tokens)
+
+    def _append(self, token_ids):
+        if self.generated >= self.max_new_tokens:
+            raise ValueError("Decode exceeds allocated max_new_tokens")
+        slots = self._next_positions(len(token_ids))
+        for seq, tok in zip(self.sequences, token_ids):
+            seq.append(tok)
+        self.used += len(token_ids)
+        return slots
+
+    def _prepare_plan(self):
+        return self.cached_plan.update(self.generated)
