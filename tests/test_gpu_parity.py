@@ -168,14 +168,20 @@ def test_misaligned_pool_and_ragged_jobs(device):
             check(out, ref, 0.008, 0.03, f"ragged/{method}")
 
 
-def test_large_row_tiles_all_kinds(device):
-    """Jobs of 20, 40, 100 and 300 requests exercise the 64/128/256-row tile kernels."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("pad", [0, 3, 8])
+def test_large_row_tiles_all_kinds(pad, dtype, device):
+    """Jobs of 20, 40, 100 and 300 requests exercise the 64/128/256-row tile kernels.
+
+    The pool capacity is 1016 + pad tokens: a multiple of 8 (pad 0, 8) selects the
+    LDS-transpose kernels, pad 3 the register-transpose kernels for unaligned pools.
+    """
     tree = KVTree.synthetic([-1, 0, 0, 0, 0], [700, 90, 33, 64, 129],
                             [1] * 20 + [2] * 40 + [3] * 100 + [4] * 140)
-    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 9)
+    q, k, v = make_inputs(tree, 32, 8, 128, dtype, 9, tcap=tree.storage_tokens + pad)
     ref = oracle_fp32(q, k, v, tree)
     for model in (CostModel(max_query_rows=1200, kv_split=512), CostModel(max_query_rows=256, kv_split=190)):
-        say("large-tiles", model.max_query_rows)
+        say("large-tiles", pad, dtype, model.max_query_rows)
         out = run(tree, "fixed", model, q, k, v, device, (32, 8, 128))
         check(out, ref, 0.008, 0.03, "large-tiles")
 

@@ -1,0 +1,145 @@
+"""Qwen3 adapter (reference src/tree_attention/qwen.py) on tiny random models.
+
+The reference's own check (scripts/check_qwen.py:21-57) decodes a tiny random
+Qwen3 (2 layers, hidden 128, 4 Q / 2 KV heads, d = 32, fp16) through the
+shared pools and compares every step's logits with a full-sequence forward of
+the same model at atol .004 / rtol .02.  The CPU tests below run the same
+protocol in fp32 with the attention call swapped for the oracle on the pools,
+which pins the adapter's pool layout, tail positions, RoPE positions and plan
+handling without a GPU; the GPU tests run the HIP kernels.
+"""
+import pytest
+import torch
+
+transformers = pytest.importorskip("transformers")
+from transformers import Qwen3Config, Qwen3ForCausalLM  # noqa: E402
+
+import tree_attention.qwen as integration  # noqa: E402
+from oracle.attention_oracle import relative_l2, request_attention  # noqa: E402
+from tree_attention import KVTree  # noqa: E402
+
+SEQUENCES = [[1, 2, 3, 4, 5], [1, 2, 3, 8], [1, 2, 3, 4, 5], [7, 8, 9, 10, 11, 12]]
+METHODS = ("request", "fixed", "greedy", "cube")
+
+
+def tiny_model(dtype, device):
+    torch.manual_seed(2026)
+    cfg = Qwen3Config(vocab_size=128, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=32)
+    return Qwen3ForCausalLM(cfg).to(dtype=dtype, device=device).eval()
+
+
+def context_paths(decoder):
+    """Physical positions each request attends to after the last step (model_checks.py:22-26)."""
+    if isinstance(decoder, integration.CachedPrefixDecoder):
+        return [path + tuple(decoder.prefix_size + r * decoder.max_new_tokens + t for t in range(decoder.generated))
+                for r, path in enumerate(decoder.tree.paths)]
+    return decoder.tree.paths
+
+
+def full_forward_logits(model, sequences, device):
+    with torch.inference_mode():
+        return torch.stack([model(torch.tensor([s], device=device), use_cache=False).logits[0, -1]
+                            for s in sequences])
+
+
+class OracleAttention:
+    """Stand-in for ``attention_matrix`` that evaluates the FP32 oracle on the pools."""
+
+    def __init__(self, decoder):
+        self.decoder = decoder
+        self.calls = 0
+
+    def __call__(self, q, kp, vp, prepared):
+        self.calls += 1
+        paths = context_paths(self.decoder)
+        out = request_attention(q.cpu(), kp.permute(2, 0, 1).cpu(), vp.permute(1, 0, 2).cpu(), KVTree([], paths))
+        prepared.out.copy_(out)
+        return prepared.out
+
+
+@pytest.mark.parametrize("cached", [False, True])
+@pytest.mark.parametrize("method", METHODS)
+def test_decode_matches_full_forward_cpu(method, cached, monkeypatch):
+    model = tiny_model(torch.float32, "cpu")
+    cls = integration.CachedPrefixDecoder if cached else integration.SharedKVDecoder
+    decoder = cls(model, SEQUENCES, 3, method)
+    stand_in = OracleAttention(decoder)
+    monkeypatch.setattr(integration, "attention_matrix", stand_in)
+    torch.testing.assert_close(decoder.logits, full_forward_logits(model, decoder.sequences, "cpu"),
+                               atol=1e-4, rtol=1e-4)
+    for step in range(3):
+        tokens = decoder.logits.argmax(-1).tolist()
+        actual = decoder.step(tokens)
+        reference = full_forward_logits(model, decoder.sequences, "cpu")
+        torch.testing.assert_close(actual, reference, atol=1e-4, rtol=1e-4, msg=lambda m: f"step {step}: {m}")
+    assert stand_in.calls == 3 * model.config.num_hidden_layers
+    # the original attention forwards are back in place
+    for layer, original in zip(model.model.layers, decoder.original):
+        assert layer.self_attn.forward == original
+
+
+def test_pool_layout_and_capacity_cpu(monkeypatch):
+    model = tiny_model(torch.float32, "cpu")
+    decoder = integration.SharedKVDecoder(model, SEQUENCES, 2, "cube")
+    tree = decoder.tree
+    assert tree.storage_tokens == 12 and decoder.prefix_size == 12
+    assert decoder.capacity == 12 + 4 * 2
+    kp, vp = decoder.pools[0]
+    assert kp.shape == (2, 32, decoder.capacity) and vp.shape == (2, decoder.capacity, 32)
+    monkeypatch.setattr(integration, "attention_matrix", OracleAttention(decoder))
+    decoder.step([0, 1, 2, 3])
+    decoder.step([4, 5, 6, 7])
+    # request r's decode tokens sit at prefix + r * max_new + step
+    assert [decoder.tree.paths[r][-2:] for r in range(4)] == [(12 + 2 * r, 13 + 2 * r) for r in range(4)]
+    with pytest.raises(ValueError, match="max_new_tokens"):
+        decoder.step([0, 0, 0, 0])
+    cached = integration.CachedPrefixDecoder(model, SEQUENCES, 1, "fixed")
+    monkeypatch.setattr(integration, "attention_matrix", OracleAttention(cached))
+    cached.step([1, 1, 1, 1])
+    with pytest.raises(ValueError, match="max_new_tokens"):
+        cached.step([1, 1, 1, 1])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("cached", [False, True])
+def test_decode_matches_full_forward_gpu(cached, dtype, device):
+    """scripts/check_qwen.py protocol on the HIP kernels: 3 greedy steps, all four methods."""
+    model = tiny_model(dtype, device)
+    cls = integration.CachedPrefixDecoder if cached else integration.SharedKVDecoder
+    # fp16: the reference's tolerance.  bf16 (not in the reference's check): its
+    # unit roundoff is 8x fp16's; logits of this model are below 1, where one bf16
+    # ulp is 0.0039, so four ulps are allowed.
+    atol, rtol = (0.004, 0.02) if dtype == torch.float16 else (0.016, 0.02)
+    for method in METHODS:
+        decoder = cls(model, SEQUENCES, 3, method)
+        for step in range(3):
+            tokens = decoder.logits.argmax(-1).tolist()
+            actual = decoder.step(tokens)
+            reference = full_forward_logits(model, decoder.sequences, device)
+            torch.testing.assert_close(actual, reference, atol=atol, rtol=rtol,
+                                       msg=lambda m: f"{method} step {step}: {m}")
+
+
+@pytest.mark.gpu
+def test_per_layer_attention_vs_oracle_gpu(device, monkeypatch):
+    """scripts/model_checks.py:42-64: every layer's tree attention vs FP32 on the same Q/K/V."""
+    model = tiny_model(torch.bfloat16, device)
+    decoder = integration.CachedPrefixDecoder(model, SEQUENCES, 4, "cube")
+    original = integration.attention_matrix
+    errors = []
+
+    def checked(q, kp, vp, prepared):
+        actual = original(q, kp, vp, prepared)
+        ref = request_attention(q.float().cpu(), kp.permute(2, 0, 1).float().cpu(),
+                                vp.permute(1, 0, 2).float().cpu(), KVTree([], context_paths(decoder)))
+        errors.append(relative_l2(actual.cpu(), ref))
+        torch.testing.assert_close(actual.cpu(), ref.to(actual.dtype), atol=0.008, rtol=0.03)
+        return actual
+
+    monkeypatch.setattr(integration, "attention_matrix", checked)
+    for _ in range(4):
+        decoder.step(decoder.logits.argmax(-1).tolist())
+    assert len(errors) == 4 * model.config.num_hidden_layers
+    assert max(errors) <= 3e-3, errors

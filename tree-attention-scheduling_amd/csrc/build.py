@@ -3,29 +3,39 @@
     python tree-attention-scheduling_amd/csrc/build.py
 
 Uses hipcc directly; no CMake, no JIT cache.  The library is placed in-tree so
-it travels with the source snapshot to the GPU machine.
+it travels with the source snapshot to the GPU machine.  Each translation unit
+has its own code-generation flags (see ``SOURCES``); the objects are linked
+into one shared library.
 """
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 PKG = HERE.parent / "tree_attention"
 INCLUDE = HERE.parent.parent / "include"
 LIB = PKG / "libtree_attn.so"
-SOURCES = [HERE / "tree_attn.hip"]
 
-FLAGS = [
-    "-O3", "-std=c++20", "--offload-arch=gfx950", "-fPIC", "-shared",
+COMMON = [
+    "-O3", "-std=c++20", "--offload-arch=gfx950", "-fPIC",
     "-mcode-object-version=5",
     # packed-FP32 VALU forms are kept out of every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA accumulators in VGPRs: every kernel fits in 256 VGPRs, and the
-    # AGPR form made the allocator copy O between register files each step
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function",
+]
+# (source, extra flags).  MFMA accumulators in VGPRs: every kernel fits in 256
+# VGPRs, and with accumulators in AGPRs the allocator copied O between the two
+# register files every step (the rescale multiplies O on the VALU).
+# segment_tile.hip also builds with -fno-honor-nans: its row maxima then
+# compile to v_max3_f32 chains without a canonicalising v_max per input; the
+# kernel never produces NaN scores (masked tokens are selected to -inf).
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+SOURCES = [
+    (HERE / "tree_attn.hip", VGPR_FORM),
+    (HERE / "segment_tile.hip", VGPR_FORM + ["-fno-honor-nans"]),
 ]
 
 
@@ -36,9 +46,7 @@ def hipcc() -> str:
     return found
 
 
-def build(verbose: bool = False) -> Path:
-    tmp = LIB.with_name(LIB.name + f".tmp{os.getpid()}")
-    cmd = [hipcc(), *FLAGS, f"-I{INCLUDE}", *map(str, SOURCES), "-o", str(tmp)]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -46,9 +54,32 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
     if verbose and res.stderr.strip():
         print(res.stderr, file=sys.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+
+
+def build(verbose: bool = False, out: Path | None = None, defines=()) -> Path:
+    """Compile every source and link ``out`` (default: the in-tree library)."""
+    target = Path(out) if out is not None else LIB
+    tmp = target.with_name(target.name + f".tmp{os.getpid()}")
+    with tempfile.TemporaryDirectory() as work:
+        objs = []
+        for src, extra in SOURCES:
+            obj = Path(work) / (src.stem + ".o")
+            _run([hipcc(), *COMMON, *extra, *[f"-D{d}" for d in defines], f"-I{INCLUDE}", f"-I{HERE}",
+                  "-c", str(src), "-o", str(obj)], verbose)
+            objs.append(str(obj))
+        _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
+    os.replace(tmp, target)
+    return target
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    args = sys.argv[1:]
+    out = None
+    defines = []
+    while args:
+        a = args.pop(0)
+        if a == "-o":
+            out = Path(args.pop(0))
+        elif a.startswith("-D"):
+            defines.append(a[2:])
+    print(build(verbose=True, out=out, defines=defines))

@@ -1,0 +1,362 @@
+// segment_tile.hip -- gfx950 kernel for large segment jobs (more than 16 query rows).
+//
+// Replaces the large phase of the reference's Triton _segment
+// (src/tree_attention/kernels.py:8-55, launched at :158-165): grouped partial
+// attention of one physical KV segment for all requests of a job, online
+// softmax in fp32, P rounded to the input dtype before PV (kernels.py:49),
+// output acc/z and the natural-log log-sum-exp m + ln z.
+//
+// One workgroup owns one (job, row tile, KV head) work item: NW waves of
+// 16*NB query rows each.  The job's tokens are streamed in 64-token tiles.
+//
+//  * HBM -> LDS without registers: a tile is D/8 1-KiB blocks of K (8 d-rows
+//    x 64 tokens each) and D/8 of V, each copied by one wave with one
+//    global_load_lds_dwordx4 (lane i fills bytes 16i..16i+15 of the block).
+//    Three LDS stages keep two tiles in flight while one is computed; each
+//    wave waits for its own copies with s_waitcnt vmcnt and the waves meet at
+//    one barrier per tile.
+//  * The lane -> 16-byte-chunk assignment inside a block is chosen so that the
+//    eight chunks one 16-lane group reads together are 128 contiguous bytes,
+//    and blocks are padded to 1152 bytes so that neighbouring groups start
+//    128 bytes apart (no LDS bank conflicts on 32- or 64-bank LDS).
+//  * MFMA operands are read with gfx950's transposing LDS load
+//    ds_read_b64_tr_b16: within a group of 16 lanes, lane 4a+b receives
+//    element b of the 8-byte chunks addressed by lanes a, a+4, a+8, a+12.
+//    Lane (g, r) addresses contraction row r/4 (+4) of its group at column
+//    4*(r%4), so every lane ends up with four consecutive contraction elements
+//    of one output row or column -- the MFMA operand layout -- straight from
+//    the pools' own layouts (K [d][token], V [token][d]).
+//  * S^T = K Q^T with v_mfma_f32_16x16x32: the C layout gives each lane four
+//    consecutive tokens of one query row, which is the B operand of the PV
+//    product O^T = V^T P^T, so P never leaves registers.
+//  * The softmax denominator is one more PV MFMA against an all-ones A
+//    operand, so z sums exactly the rounded P that multiplies V.
+//  * Softmax in base 2 with log2(e)/sqrt(D) folded into one FMA; lazy
+//    rescaling (the running maximum moves only by more than TAU).
+// Requirements (checked by the launcher): tcap % 8 == 0 and 16-byte aligned
+// pools, so every 8-token chunk of a K row is one aligned 16-byte copy.
+#include "ta_common.h"
+#include "tree_attn.h"
+
+namespace ta {
+namespace {
+
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
+#define TA_VMCNT(n) ((((n)&15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
+
+// Two transposing LDS loads -> one 8-element MFMA operand.
+__device__ inline u32x4 tr_pair(const u16 *lo, const u16 *hi) {
+    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)lo);
+    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)hi);
+    const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+    return u32x4{ua[0], ua[1], ub[0], ub[1]};
+}
+
+// LDS layout of one 64-token tile (16-bit elements): KBLK blocks of K, then
+// VBLK blocks of V, each a 1 KiB copy unit padded to BLK elements.
+//   K block b: d-rows 8b..8b+7; the 16-byte chunk c (tokens 8c..8c+7) of
+//     d-row 8b+j sits in slot 16*(c>>1) + 8*(j>>2) + 4*(c&1) + (j&3).
+//   V block b: token rows VROWS*b ..; chunk s (d = 8s..8s+7) of token row j
+//     sits in slot SV*(s>>1) + 8*(j>>2) + 4*(s&1) + (j&3).
+template <int D>
+struct Tile {
+    static constexpr int TT = 64;
+    static constexpr int BLK = 576;         // 1 KiB block + 128 B padding
+    static constexpr int KBLK = D / 8;
+    static constexpr int VROWS = 512 / D;   // token rows per V block
+    static constexpr int VBLK = TT / VROWS;
+    static constexpr int NBLK = KBLK + VBLK;
+    static constexpr int ELEMS = NBLK * BLK;
+    static constexpr int SV = 1024 / D;
+};
+
+template <int D, bool FP16, int NB, int NW>
+struct TileMath {
+    static constexpr int DB = D / 16;  // 16-row blocks of O^T
+    static constexpr int KS = D / 32;  // 32-wide k slices of QK
+    using O = Ops<FP16>;
+    using T = Tile<D>;
+
+    f32x4 o[NB][DB], z[NB];
+    float m[NB];
+
+    __device__ void reset() {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            m[nb] = NEG_INF;
+            z[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int db = 0; db < DB; ++db) o[nb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    // One pipeline step: copy the tile at pool token t0n into stage `nxt` (if
+    // `copy`), then compute the tile staged in `cur` (if `compute`).  The two
+    // stages never alias; declaring them restrict in one function lets the
+    // compiler keep the copies in flight across the reads of `cur`.
+    __device__ void step(const u16 *__restrict__ cur, u16 *__restrict__ nxt, bool copy, bool compute,
+                         const u16 *__restrict__ kp, const u16 *__restrict__ vp, int h, int tcap, int t0n, int kst,
+                         int kend, int wave, int lane, const u32x4 (&qf)[NB][KS], int koff, int voff, int lo,
+                         int hi, int g4, float c) {
+        if (copy) {
+#pragma unroll
+            for (int i = 0; i < T::NBLK / NW; ++i) {
+                const int blk = wave + i * NW;
+                const u16 *src;
+                if (blk < T::KBLK) {
+                    const int ck = 2 * (lane >> 4) + ((lane >> 2) & 1);
+                    const int d = 8 * blk + 4 * ((lane >> 3) & 1) + (lane & 3);
+                    // chunks past the pool end read its last chunk; their scores are masked
+                    src = kp + (size_t)(h * D + d) * tcap + min(t0n + 8 * ck, tcap - 8);
+                } else {
+                    const int vb = blk - T::KBLK;
+                    const int rem = lane % T::SV;
+                    const int s = 2 * (lane / T::SV) + ((rem >> 2) & 1);
+                    const int j = 4 * (rem >> 3) + (rem & 3);
+                    // rows outside the job read a row inside it: finite values, P = 0
+                    const int t = min(max(t0n + vb * T::VROWS + j, kst), kend - 1);
+                    src = vp + ((size_t)h * tcap + t) * D + 8 * s;
+                }
+                __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(nxt + blk * T::BLK), 16, 0, 0);
+            }
+        }
+        if (compute) tile(cur, qf, koff, voff, lo, hi, g4, c);
+    }
+
+    // K fragments (A operand of QK) of the 32 tokens base .. base+31:
+    // kf[b][ks] covers tokens base+16b .. +15, d = 32*ks .. +31.
+    __device__ static void load_k(const u16 *__restrict__ cur, int koff, int base, u32x4 (&kf)[2][KS]) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                // block 4*ks + g4, chunk pair base/16 + b, block rows 0-3 / 4-7
+                const u16 *ka = cur + koff + 4 * T::BLK * ks + 8 * (base + 16 * b);
+                kf[b][ks] = tr_pair(ka, ka + 64);
+            }
+    }
+
+    // S^T = K Q^T: s[nb][b] holds tokens base+16b+4*g4+i of row block nb.
+    __device__ static void qk(const u32x4 (&kf)[2][KS], const u32x4 (&qf)[NB][KS], f32x4 (&s)[NB][2]) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) s[nb][0] = s[nb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) s[nb][b] = O::mma_k32(kf[b][ks], qf[nb][ks], s[nb][b]);
+    }
+
+    // koff / voff: per-lane element offsets of the transposing loads;
+    // tokens [lo, hi) of the tile belong to the job.  Software pipeline per
+    // 32-token step k: the LDS loads of step k's V and step k+1's K are issued
+    // before step k's softmax (which hides their latency), then PV of step k
+    // and QK of step k+1 run back to back on the matrix cores.
+    __device__ void tile(const u16 *__restrict__ cur, const u32x4 (&qf)[NB][KS], int koff, int voff, int lo,
+                         int hi, int g4, float c) {
+        constexpr int STEPS = T::TT / 32;
+        const u32x4 ones = {O::ONE2, O::ONE2, O::ONE2, O::ONE2};
+        f32x4 s[NB][2];
+        {
+            u32x4 kf[2][KS];
+            load_k(cur, koff, 0, kf);
+            qk(kf, qf, s);
+        }
+#pragma unroll
+        for (int k = 0; k < STEPS; ++k) {
+            const int base = 32 * k;
+            if (base >= hi) break;
+            // V^T fragments of this step: PV k-slot j of lane group g4 is token
+            // 4*g4+j (j<4) or 16+4*g4+j-4 (j>=4), where the QK output left P.
+            u32x4 vf[DB];
+            const u16 *vrow = cur + voff + T::BLK * (T::KBLK + base / T::VROWS);
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const u16 *va = vrow + 8 * T::SV * db;
+                vf[db] = tr_pair(va, va + T::BLK * (16 / T::VROWS));
+            }
+            const bool more = k + 1 < STEPS && base + 32 < hi;
+            u32x4 kf[2][KS];
+            if (more) load_k(cur, koff, base + 32, kf);
+            if (lo > base || hi < base + 32) {  // wave-uniform: first or last step of the job
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int tok = base + 16 * b + 4 * g4 + i;
+                            if (tok < lo || tok >= hi) s[nb][b][i] = NEG_INF;
+                        }
+            }
+            // ---- softmax of every row block -> P^T fragments (B operand of PV)
+            u32x4 pb[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                float x[8];
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) x[4 * b + i] = s[nb][b][i];
+                const float lm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                                       fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+                const bool need = lm * c > m[nb] + TAU;
+                if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform, rare after the first step
+                    const float mn = fmaxf(m[nb], xor_max(lm) * c);
+                    const float alpha = fast_exp2(m[nb] - mn);
+                    z[nb] *= alpha;
+#pragma unroll
+                    for (int db = 0; db < DB; ++db) o[nb][db] *= alpha;
+                    m[nb] = mn;
+                }
+                float pr[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(__builtin_fmaf(x[i], c, -m[nb]));
+                pb[nb] = u32x4{O::pack(pr[0], pr[1]), O::pack(pr[2], pr[3]), O::pack(pr[4], pr[5]),
+                               O::pack(pr[6], pr[7])};
+            }
+            // ---- O^T += V^T P^T (each V^T fragment feeds NB MFMAs), then QK of step k+1
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) o[nb][db] = O::mma_k32(vf[db], pb[nb], o[nb][db]);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) z[nb] = O::mma_k32(ones, pb[nb], z[nb]);
+            if (more) qk(kf, qf, s);
+        }
+    }
+};
+
+template <int D, bool FP16, int NB, int NW>
+__global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
+    using T = Tile<D>;
+    using M = TileMath<D, FP16, NB, NW>;
+    constexpr int KS = M::KS;
+    constexpr int BPW = T::NBLK / NW;  // copies per wave per tile
+    static_assert(T::NBLK % NW == 0, "every wave copies the same number of blocks");
+    __shared__ __attribute__((aligned(16))) u16 lds[3 * T::ELEMS];
+
+    // Linear block L runs on XCD L % 8; give every XCD a contiguous range of
+    // items so that row tiles of one (job, head) share an L2.
+    const int total = gridDim.x;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int q8 = total >> 3, rm = total & 7;
+    const int item = xcd * q8 + min(xcd, rm) + slot;
+    const int job = p.items[3 * item], row0 = p.items[3 * item + 1], h = p.items[3 * item + 2];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row = lane & 15, g4 = lane >> 4;
+    const int kst = p.kstart[job];
+    const int ntok = max(0, min(p.klen[job], p.tcap - kst));
+    const int kend = kst + ntok;
+    const int nrows = p.qlen[job] * p.group;
+    const int wrow0 = row0 + 16 * NB * wave;
+    const bool active = wrow0 < nrows;
+
+    // Q^T fragments (B operand): lane (row, g4) holds d = 32*ks + 8*g4 .. +7.
+    u32x4 qf[NB][KS];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int rr = wrow0 + 16 * nb + row;
+        if (rr < nrows) {
+            const int lr = rr / p.group, gg = rr - lr * p.group;
+            const int rq = p.qids[(size_t)job * p.maxr + lr];
+            const u16 *src = p.q + ((size_t)rq * p.hq + h * p.group + gg) * D + 8 * g4;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) qf[nb][ks] = *(const u32x4 *)(src + 32 * ks);
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) qf[nb][ks] = u32x4{0, 0, 0, 0};
+        }
+    }
+    // Pin the Q fragments: an empty asm that "redefines" them makes the wave
+    // wait for the Q loads once, here, and not inside the tile loop behind the
+    // copies in flight.
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qf[nb][ks]));
+
+    M acc;
+    acc.reset();
+    // Lane part of the transposing-load offsets: block (K) or token group (V)
+    // g4, slot 4*((row&3)>>1) + (row>>2), 8-byte half row&1.
+    const int lane_ofs = 8 * (4 * ((row & 3) >> 1) + (row >> 2)) + 4 * (row & 1);
+    const int koff = T::BLK * g4 + lane_ofs;
+    const int voff = T::BLK * ((4 * g4) / T::VROWS) + 64 * (((4 * g4) % T::VROWS) >> 2) + lane_ofs;
+
+    const int tb0 = kst & ~7;
+    const int ntiles = ntok > 0 ? (kend - tb0 + T::TT - 1) / T::TT : 0;
+    // Iteration it copies tile it+2 and computes tile it (stage it % 3); the
+    // first two iterations only copy, so every copy comes from one call site.
+    int cs = 1;  // stage of tile it (tile -2 "sits" in stage 1)
+    for (int it = -2; it < ntiles; ++it) {
+        if (it >= 0) {
+            // this wave's copies of tile it are done once at most tile it+1's are pending
+            if (it + 1 < ntiles)
+                __builtin_amdgcn_s_waitcnt(TA_VMCNT(BPW));
+            else
+                __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
+            __builtin_amdgcn_s_barrier();  // every copy of tile it landed; stage of tile it-1 is free
+        }
+        const int ns = cs == 0 ? 2 : cs - 1;  // stage of tile it+2 (that of tile it-1)
+        const int t0 = tb0 + it * T::TT;
+        acc.step(lds + cs * T::ELEMS, lds + ns * T::ELEMS, it + 2 < ntiles, it >= 0 && active, p.kp, p.vp, h,
+                 p.tcap, t0 + 2 * T::TT, kst, kend, wave, lane, qf, koff, voff, max(0, kst - t0),
+                 min(T::TT, kend - t0), g4, p.scale_log2);
+        cs = cs == 2 ? 0 : cs + 1;
+    }
+
+    if (!active) return;
+    const int rb = p.rowbase[job];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int grow = wrow0 + 16 * nb + row;
+        if (grow >= nrows) continue;
+        const int lr = grow / p.group, gg = grow - lr * p.group;
+        const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
+        float *dst = p.part + prow * D + 4 * g4;
+        const bool any = acc.m[nb] != NEG_INF;
+        const float zr = acc.z[nb][0];
+        const float inv = any ? 1.f / zr : 0.f;
+#pragma unroll
+        for (int db = 0; db < M::DB; ++db) *(f32x4 *)(dst + 16 * db) = acc.o[nb][db] * inv;
+        if (g4 == 0) p.lse[prow] = any ? (acc.m[nb] + __builtin_amdgcn_logf(zr)) * LN2 : NEG_INF;
+    }
+}
+
+template <int D, bool FP16>
+hipError_t launch_d(const SegParams &sp, int kind, hipStream_t stream) {
+    switch (kind) {
+        case TA_LARGE64:
+            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 1, 4>), dim3(sp.n_items), dim3(256), 0, stream, sp);
+            break;
+        case TA_LARGE128:
+            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 2, 4>), dim3(sp.n_items), dim3(256), 0, stream, sp);
+            break;
+        case TA_LARGE256:
+            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 2, 8>), dim3(sp.n_items), dim3(512), 0, stream, sp);
+            break;
+        default:
+            return hipErrorNotSupported;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_tile(const SegParams &sp, int kind, int d, bool fp16, hipStream_t stream) {
+    if (sp.tcap % 8 != 0) return hipErrorNotSupported;
+    switch (d) {
+        case 128: return fp16 ? launch_d<128, true>(sp, kind, stream) : launch_d<128, false>(sp, kind, stream);
+        case 64: return fp16 ? launch_d<64, true>(sp, kind, stream) : launch_d<64, false>(sp, kind, stream);
+        case 32: return fp16 ? launch_d<32, true>(sp, kind, stream) : launch_d<32, false>(sp, kind, stream);
+        default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace ta

@@ -1,0 +1,94 @@
+// ta_common.h -- device helpers and launch arguments shared by the gfx950
+// segment kernels of libtree_attn.so (internal; not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ta {
+
+using u16 = unsigned short;
+using u32 = unsigned int;
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+typedef u32 u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr float LN2 = 0.69314718055994530942f;
+constexpr float NEG_INF = -__builtin_inff();
+
+// Lazy rescaling threshold in log2 units: a row's running maximum is only
+// raised when a score exceeds it by more than TAU, so exponentials stay
+// <= 2^TAU and the accumulator rescale (a pass over all of O) is skipped on
+// almost every step.  The final log-sum-exp is exact for any stale maximum.
+constexpr float TAU = 8.0f;
+
+// MFMA and packing for one 16-bit input type.
+template <bool FP16>
+struct Ops;
+
+template <>
+struct Ops<false> {  // bfloat16
+    __device__ static f32x4 mma_k32(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+    __device__ static f32x4 mma_k16(u32x2 a, u32x2 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                         __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+    }
+    __device__ static u32 pack(float lo, float hi) {
+        bf16x2 v = {(__bf16)lo, (__bf16)hi};
+        return __builtin_bit_cast(u32, v);
+    }
+    static constexpr u32 ONE2 = 0x3F803F80u;  // two 1.0 values
+};
+
+template <>
+struct Ops<true> {  // float16
+    __device__ static f32x4 mma_k32(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+    __device__ static f32x4 mma_k16(u32x2 a, u32x2 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                     __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+    }
+    __device__ static u32 pack(float lo, float hi) {
+        f16x2 v = {(_Float16)lo, (_Float16)hi};
+        return __builtin_bit_cast(u32, v);
+    }
+    static constexpr u32 ONE2 = 0x3C003C00u;
+};
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ inline float xor_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+
+__device__ inline float xor_sum(float v) {
+    v += __shfl_xor(v, 16);
+    return v + __shfl_xor(v, 32);
+}
+
+// Launch arguments of every segment kernel.
+struct SegParams {
+    const u16 *q, *kp, *vp;
+    const int32_t *qids, *kstart, *qlen, *klen, *rowbase, *items;
+    float *part, *lse;
+    int n_items, hq, hk, group, tcap, maxr;
+    float scale_log2;  // log2(e) / sqrt(D)
+};
+
+// Large-job launcher of segment_tile.hip (gfx950 LDS-transpose kernels).
+// Returns hipErrorNotSupported when the shape is outside what it handles.
+hipError_t launch_tile(const SegParams &sp, int kind, int d, bool fp16, hipStream_t stream);
+
+}  // namespace ta

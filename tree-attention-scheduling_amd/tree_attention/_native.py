@@ -3,11 +3,13 @@
 The library is loaded on first use.  ``torch`` is imported first so that the
 library binds to the HIP runtime torch already loaded (both carry the soname
 ``libamdhip64.so.7``); stream handles from ``torch.cuda`` are then valid here.
-There is no fallback: if the library is missing, every call raises.
+There is no fallback: if the library is missing, every call raises.  The
+environment variable ``TREE_ATTN_LIB`` selects another build of the library.
 """
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
@@ -48,7 +50,7 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         if _lib is not None and path is None:
             return _lib
         import torch  # noqa: F401  -- bind to torch's HIP runtime first
-        target = Path(path) if path is not None else LIB_PATH
+        target = Path(path) if path is not None else Path(os.environ.get("TREE_ATTN_LIB", LIB_PATH))
         if not target.exists():
             raise RuntimeError(
                 f"tree_attn native library not found at {target}; build it with "

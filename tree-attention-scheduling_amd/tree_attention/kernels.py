@@ -38,10 +38,11 @@ _DTYPES = {torch.bfloat16: _native.TA_BF16, torch.float16: _native.TA_FP16}
 SMALL_ROWS = 16  # rows of one MFMA block; same threshold as kernels.py:109-110
 
 
-def _large_kind(rows: int) -> int:
-    if rows <= 64:
+def _large_kind(rows: int, tile_rows: int = 256) -> int:
+    """Row-tile kernel for a job with ``rows`` query rows (tiles of at most ``tile_rows``)."""
+    if rows <= 64 or tile_rows <= 64:
         return _native.TA_LARGE64
-    if rows <= 128:
+    if rows <= 128 or tile_rows <= 128:
         return _native.TA_LARGE128
     return _native.TA_LARGE256
 
@@ -68,13 +69,13 @@ class PreparedPlan:
     metadata: torch.Tensor | None = None
 
 
-def _build_items(jobs, small_jobs, group, kvheads):
+def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256):
     """Work items per kernel kind as int32 arrays (see module docstring)."""
     small = np.arange(small_jobs, dtype=np.int32)
     large = {k: [] for k in _native.KIND_ROWS}
     for j in range(small_jobs, len(jobs)):
         rows = len(jobs[j].requests) * group
-        kind = _large_kind(rows)
+        kind = _large_kind(rows, tile_rows)
         tile = _native.KIND_ROWS[kind]
         for h in range(kvheads):
             for row0 in range(0, rows, tile):
@@ -85,11 +86,13 @@ def _build_items(jobs, small_jobs, group, kvheads):
     return items
 
 
-def prepare(plan: Plan, q: torch.Tensor) -> PreparedPlan:
+def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256) -> PreparedPlan:
     """Lower ``plan`` to device metadata and scratch for queries shaped like ``q``.
 
     Mirrors kernels.py:103-141: physical jobs, stable small-first order, one
-    host-to-device copy of all int32 metadata, scratch allocated once.  Raises
+    host-to-device copy of all int32 metadata, scratch allocated once.
+    ``tile_rows`` (64, 128 or 256) caps the query rows one workgroup of the
+    large-job kernels handles; it changes the work split, not the result.  Raises
     ``ValueError`` for jobs without requests or tokens, request ids outside
     ``q`` and token runs that are not consecutive physical ids.
     """
@@ -136,7 +139,7 @@ def prepare(plan: Plan, q: torch.Tensor) -> PreparedPlan:
     for r, values in enumerate(slots):
         slot_array[r, :len(values)] = values
     counts = np.array([len(s) for s in slots], dtype=np.int32)
-    items = _build_items(jobs, small_jobs, group, kvheads)
+    items = _build_items(jobs, small_jobs, group, kvheads, tile_rows)
 
     arrays = [qids, kids, qlen, klen, slot_array, counts, rowbase] + [items[k] for k in sorted(items)]
     dev = q.device

@@ -4,7 +4,9 @@
         --cost-model mi355x --kernel large256 --iters 20
 
 ``--kernel`` is one of ``small``, ``large64``, ``large128``, ``large256``,
-``merge`` or ``layer`` (the whole attention_matrix call).  K/V rotate over
+``merge``, ``layer`` (the whole attention_matrix call) or ``copy`` (a plain
+device-to-device copy of ``--copy-mib`` MiB, the reference point that scales
+rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes).  K/V rotate over
 ``--pools`` copies so repeated launches read HBM, not the MALL.  Prints the
 mean device time per launch measured with HIP events.
 """
@@ -28,10 +30,12 @@ def main(argv=None):
     ap.add_argument("--shape", default="wide_long")
     ap.add_argument("--method", default="cube")
     ap.add_argument("--cost-model", default="mi355x", choices=["mi355x", "reference"])
-    ap.add_argument("--kernel", default="layer", choices=sorted(KINDS) + ["merge", "layer"])
+    ap.add_argument("--kernel", default="layer", choices=sorted(KINDS) + ["merge", "layer", "copy"])
+    ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--pools", type=int, default=8)
     ap.add_argument("--heads", default="32,8,128")
+    ap.add_argument("--tile-rows", type=int, default=256)
     ap.add_argument("--param", action="append", default=[],
                     help="CostModel field override, e.g. --param kv_split=1024 (repeatable)")
     args = ap.parse_args(argv)
@@ -49,12 +53,18 @@ def main(argv=None):
     v = torch.randn(tree.storage_tokens, hk, d, generator=g).bfloat16().to(dev)
     kp, vp = pack_kv(k, v)
     pools = [(kp, vp)] + [(kp.clone(), vp.clone()) for _ in range(args.pools - 1)]
-    prepared = prepare(schedule(tree, hq, hk, d, args.method, model), q)
+    prepared = prepare(schedule(tree, hq, hk, d, args.method, model), q, args.tile_rows)
     attention_matrix(q, kp, vp, prepared)  # partials exist before a lone merge
+
+    if args.kernel == "copy":
+        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
 
     def launch(i):
         kpi, vpi = pools[i % len(pools)]
-        if args.kernel == "layer":
+        if args.kernel == "copy":
+            dst.copy_(src)
+        elif args.kernel == "layer":
             attention_matrix(q, kpi, vpi, prepared)
         elif args.kernel == "merge":
             merge(prepared)
@@ -72,7 +82,7 @@ def main(argv=None):
     torch.cuda.synchronize()
     print(json.dumps({"kernel": args.kernel, "shape": args.shape, "method": args.method,
                       "params": {f: getattr(model, f) for f in ("kv_split", "max_query_rows")},
-                      "iters": args.iters, "us_per_launch": start.elapsed_time(end) * 1e3 / args.iters,
+                      "tile_rows": args.tile_rows, "iters": args.iters, "us_per_launch": start.elapsed_time(end) * 1e3 / args.iters,
                       "items": list(prepared.abi.n_items)}), flush=True)
 
 
