@@ -39,11 +39,11 @@ extern "C" {
 #define TA_BF16 0
 #define TA_FP16 1
 
-/* segment work-item kinds */
-#define TA_SMALL 0      /* jobs with <= 16 query rows; items = job ids, grid (n, hk)        */
-#define TA_LARGE64 1    /* row tiles of 64 rows;  items = (job, first row, kv head) triples */
-#define TA_LARGE128 2   /* row tiles of 128 rows; items = (job, first row, kv head) triples */
-#define TA_LARGE256 3   /* row tiles of 256 rows; items = (job, first row, kv head) triples */
+/* segment work-item kinds; items are (job, first query row, kv head) triples */
+#define TA_SMALL 0      /* jobs with <= 16 query rows (first row 0), one wave each */
+#define TA_LARGE64 1    /* row tiles of 64 rows  */
+#define TA_LARGE128 2   /* row tiles of 128 rows */
+#define TA_LARGE256 3   /* row tiles of 256 rows */
 
 #define TA_ERR_ARG 1001      /* null pointer, bad size or unsupported shape */
 #define TA_ERR_ALIGN 1002    /* q / kp / vp / part / out not 16-byte aligned */
@@ -59,8 +59,8 @@ typedef struct ta_plan {
     const int32_t *rowbase;   /* [njobs] first partial slot of each job            */
     const int32_t *slots;     /* [nreq * maxs] partial slots of each request       */
     const int32_t *counts;    /* [nreq] number of slots of each request            */
-    const int32_t *items[4];  /* work items per kind TA_SMALL .. TA_LARGE256       */
-    int32_t n_items[4];
+    const int32_t *items[4];  /* work-item triples per kind TA_SMALL .. TA_LARGE256 */
+    int32_t n_items[4];       /* number of triples per kind                        */
     float *part;
     float *lse;
     int32_t njobs, maxr, maxs, nreq, nslot;

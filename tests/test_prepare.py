@@ -29,7 +29,9 @@ def test_metadata_layout_small_first_and_compact_slots():
         assert {slot_owner[s] for s in p.slots[r, :counts[r]].tolist()} == {r}
     assert p.part.shape == (sum(qlen), 32, 128) and p.lse.shape == (sum(qlen), 32)
     # work items: 128 small jobs; large jobs of 16 requests = 64 rows -> one 64-row tile per head
-    assert p.abi.n_items[_native.TA_SMALL] == 128
+    assert p.abi.n_items[_native.TA_SMALL] == 128 * 8
+    small = p.items[_native.TA_SMALL].view(-1, 3).tolist()
+    assert sorted(small) == [[j, 0, h] for j in range(128) for h in range(8)]
     assert p.abi.n_items[_native.TA_LARGE64] == 128 * 8
     items = p.items[_native.TA_LARGE64].view(-1, 3).tolist()
     assert sorted(set((j, h) for j, _, h in items)) == [(j, h) for j in range(128, 256) for h in range(8)]

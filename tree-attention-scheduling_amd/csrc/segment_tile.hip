@@ -7,14 +7,15 @@
 // output acc/z and the natural-log log-sum-exp m + ln z.
 //
 // One workgroup owns one (job, row tile, KV head) work item: NW waves of
-// 16*NB query rows each.  The job's tokens are streamed in 64-token tiles.
+// 16*NB query rows each (jobs with at most 16 rows: one wave, NB = 1).  The
+// job's tokens are streamed in 64-token tiles.
 //
 //  * HBM -> LDS without registers: a tile is D/8 1-KiB blocks of K (8 d-rows
 //    x 64 tokens each) and D/8 of V, each copied by one wave with one
 //    global_load_lds_dwordx4 (lane i fills bytes 16i..16i+15 of the block).
-//    Three LDS stages keep two tiles in flight while one is computed; each
-//    wave waits for its own copies with s_waitcnt vmcnt and the waves meet at
-//    one barrier per tile.
+//    Three LDS stages keep two tiles in flight while one is computed (one-wave
+//    workgroups of small jobs use one stage, so that four share a CU); each wave waits for its own copies with s_waitcnt vmcnt
+//    and the waves meet at one barrier per tile.
 //  * The lane -> 16-byte-chunk assignment inside a block is chosen so that the
 //    eight chunks one 16-lane group reads together are 128 contiguous bytes,
 //    and blocks are padded to 1152 bytes so that neighbouring groups start
@@ -101,7 +102,14 @@ struct TileMath {
                          const u16 *__restrict__ kp, const u16 *__restrict__ vp, int h, int tcap, int t0n, int kst,
                          int kend, int wave, int lane, const u32x4 (&qf)[NB][KS], int koff, int voff, int lo,
                          int hi, int g4, float c) {
-        if (copy) {
+        if (copy) this->copy(nxt, kp, vp, h, tcap, t0n, kst, kend, wave, lane);
+        if (compute) tile(cur, qf, koff, voff, lo, hi, g4, c);
+    }
+
+    // Copy the tile at pool token t0n into stage `st` (this wave's blocks).
+    __device__ static void copy(u16 *st, const u16 *__restrict__ kp, const u16 *__restrict__ vp, int h,
+                                int tcap, int t0n, int kst, int kend, int wave, int lane) {
+        {
 #pragma unroll
             for (int i = 0; i < T::NBLK / NW; ++i) {
                 const int blk = wave + i * NW;
@@ -120,10 +128,9 @@ struct TileMath {
                     const int t = min(max(t0n + vb * T::VROWS + j, kst), kend - 1);
                     src = vp + ((size_t)h * tcap + t) * D + 8 * s;
                 }
-                __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(nxt + blk * T::BLK), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + blk * T::BLK), 16, 0, 0);
             }
         }
-        if (compute) tile(cur, qf, koff, voff, lo, hi, g4, c);
     }
 
     // K fragments (A operand of QK) of the 32 tokens base .. base+31:
@@ -231,14 +238,15 @@ struct TileMath {
     }
 };
 
-template <int D, bool FP16, int NB, int NW>
+template <int D, bool FP16, int NB, int NW, int STAGES>
 __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
     using T = Tile<D>;
     using M = TileMath<D, FP16, NB, NW>;
     constexpr int KS = M::KS;
     constexpr int BPW = T::NBLK / NW;  // copies per wave per tile
     static_assert(T::NBLK % NW == 0, "every wave copies the same number of blocks");
-    __shared__ __attribute__((aligned(16))) u16 lds[3 * T::ELEMS];
+    static_assert(STAGES >= 1 && STAGES <= 3, "one to three LDS stages");
+    __shared__ __attribute__((aligned(16))) u16 lds[STAGES * T::ELEMS];
 
     // Linear block L runs on XCD L % 8; give every XCD a contiguous range of
     // items so that row tiles of one (job, head) share an L2.
@@ -291,24 +299,39 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
 
     const int tb0 = kst & ~7;
     const int ntiles = ntok > 0 ? (kend - tb0 + T::TT - 1) / T::TT : 0;
-    // Iteration it copies tile it+2 and computes tile it (stage it % 3); the
-    // first two iterations only copy, so every copy comes from one call site.
-    int cs = 1;  // stage of tile it (tile -2 "sits" in stage 1)
-    for (int it = -2; it < ntiles; ++it) {
+    if (STAGES == 1) {
+        // one stage (one-wave workgroups, four per CU): copy, wait, compute
+        for (int it = 0; it < ntiles; ++it) {
+            const int t0 = tb0 + it * T::TT;
+            if (it > 0) __builtin_amdgcn_s_barrier();  // every wave is done with the previous tile
+            acc.copy(lds, p.kp, p.vp, h, p.tcap, t0, kst, kend, wave, lane);
+            __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
+            __builtin_amdgcn_s_barrier();
+            if (active) acc.tile(lds, qf, koff, voff, max(0, kst - t0), min(T::TT, kend - t0), g4, p.scale_log2);
+        }
+    } else {
+    // Iteration it copies tile it+STAGES-1 and computes tile it (stage it %
+    // STAGES); the first STAGES-1 iterations only copy, so every copy comes
+    // from one call site.
+    constexpr int AHEAD = STAGES > 1 ? STAGES - 1 : 1;
+    int cs = STAGES - AHEAD;  // stage of tile it, starting at it = -AHEAD
+    for (int it = -AHEAD; it < ntiles; ++it) {
         if (it >= 0) {
-            // this wave's copies of tile it are done once at most tile it+1's are pending
-            if (it + 1 < ntiles)
+            // this wave's copies of tile it are done once at most those of the
+            // tiles after it (issued, at most AHEAD-1 of them) are pending
+            if (AHEAD == 2 && it + 1 < ntiles)
                 __builtin_amdgcn_s_waitcnt(TA_VMCNT(BPW));
             else
                 __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
             __builtin_amdgcn_s_barrier();  // every copy of tile it landed; stage of tile it-1 is free
         }
-        const int ns = cs == 0 ? 2 : cs - 1;  // stage of tile it+2 (that of tile it-1)
+        const int ns = cs == 0 ? STAGES - 1 : cs - 1;  // stage of tile it+AHEAD (that of tile it-1)
         const int t0 = tb0 + it * T::TT;
-        acc.step(lds + cs * T::ELEMS, lds + ns * T::ELEMS, it + 2 < ntiles, it >= 0 && active, p.kp, p.vp, h,
-                 p.tcap, t0 + 2 * T::TT, kst, kend, wave, lane, qf, koff, voff, max(0, kst - t0),
+        acc.step(lds + cs * T::ELEMS, lds + ns * T::ELEMS, it + AHEAD < ntiles, it >= 0 && active, p.kp, p.vp, h,
+                 p.tcap, t0 + AHEAD * T::TT, kst, kend, wave, lane, qf, koff, voff, max(0, kst - t0),
                  min(T::TT, kend - t0), g4, p.scale_log2);
-        cs = cs == 2 ? 0 : cs + 1;
+        cs = cs == STAGES - 1 ? 0 : cs + 1;
+    }
     }
 
     if (!active) return;
@@ -332,14 +355,17 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
 template <int D, bool FP16>
 hipError_t launch_d(const SegParams &sp, int kind, hipStream_t stream) {
     switch (kind) {
+        case TA_SMALL:  // one wave per (job, head); one stage so that four fit on a CU
+            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 1, 1, 1>), dim3(sp.n_items), dim3(64), 0, stream, sp);
+            break;
         case TA_LARGE64:
-            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 1, 4>), dim3(sp.n_items), dim3(256), 0, stream, sp);
+            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 1, 4, 3>), dim3(sp.n_items), dim3(256), 0, stream, sp);
             break;
         case TA_LARGE128:
-            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 2, 4>), dim3(sp.n_items), dim3(256), 0, stream, sp);
+            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 2, 4, 3>), dim3(sp.n_items), dim3(256), 0, stream, sp);
             break;
         case TA_LARGE256:
-            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 2, 8>), dim3(sp.n_items), dim3(512), 0, stream, sp);
+            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 2, 8, 3>), dim3(sp.n_items), dim3(512), 0, stream, sp);
             break;
         default:
             return hipErrorNotSupported;

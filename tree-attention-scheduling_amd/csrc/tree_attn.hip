@@ -299,7 +299,7 @@ __global__ __launch_bounds__(SMALL_NT) void seg_small_kernel(SegParams p) {
     __shared__ __attribute__((aligned(16))) u16 lds[S::ELEMS];
     const int lane = threadIdx.x;
     const int row = lane & 15, g4 = lane >> 4;
-    const int total = p.n_items * p.hk;
+    const int total = p.n_items;
     const float c = p.scale_log2;
     const int stride = gridDim.x;
 
@@ -309,8 +309,8 @@ __global__ __launch_bounds__(SMALL_NT) void seg_small_kernel(SegParams p) {
     };
     auto decode = [&](int idx) {
         Item it;
-        it.job = p.items[idx / p.hk];
-        it.h = idx - (idx / p.hk) * p.hk;
+        it.job = p.items[3 * idx];
+        it.h = p.items[3 * idx + 2];
         it.kst = p.kstart[it.job];
         it.ntok = max(0, min(p.klen[it.job], p.tcap - it.kst));
         it.ntiles = (it.ntok + SMALL_TT - 1) / SMALL_TT;
@@ -434,12 +434,13 @@ __global__ __launch_bounds__(64 * NW) void seg_large_kernel(SegParams p) {
 }
 
 // ------------------------------------------------------------------ merge
-// One workgroup per (request, group of MH query heads): the MH*D partial
-// elements of one slot are contiguous, so every slot is one coalesced
-// 16-byte-per-thread sweep.  The request's slot list, the log-sum-exp values
-// and the normalised merge weights are staged in LDS first; the slot loop is
-// unrolled so several slots' loads are in flight per thread.
-constexpr int MERGE_MAX_SLOTS = 256;
+// One workgroup per (request, group of MH query heads); thread (head, d4)
+// owns four head-dim elements of one query head.  The slot list is uniform
+// per workgroup (scalar loads), and each thread reads the log-sum-exp and the
+// 16-byte partial slice of CHUNK slots at once and merges them online in
+// registers: slots -> (lse, partials) is the only chain of dependent memory
+// round trips; no LDS and no barriers.
+constexpr int MERGE_CHUNK = 8;
 
 template <int D, bool FP16>
 __global__ __launch_bounds__(NT) void merge_kernel(const float *__restrict__ part, const float *__restrict__ lse,
@@ -448,76 +449,48 @@ __global__ __launch_bounds__(NT) void merge_kernel(const float *__restrict__ par
                                                    int hq, int maxs) {
     constexpr int TPH = D / 4;    // threads per head
     constexpr int MH = NT / TPH;  // heads per workgroup
-    __shared__ int sl[MERGE_MAX_SLOTS];
-    __shared__ float w[MERGE_MAX_SLOTS * MH];
-    __shared__ float mh[MH], invz[MH];
-
+    constexpr float LOG2E = 1.44269504088896341f;
     const int r = blockIdx.x;
-    const int h0 = blockIdx.y * MH;
-    const int nh = min(MH, hq - h0);
     const int tid = threadIdx.x;
+    const int hl = tid / TPH, d4 = tid % TPH;
+    const int head = blockIdx.y * MH + hl;
+    if (head >= hq) return;
     const int cnt = counts[r];
     const int32_t *slr = slots + (size_t)r * maxs;
-    const int hl = tid / TPH, d4 = tid % TPH;
-    const int head = h0 + hl;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const float *src = part + (size_t)head * D + 4 * d4;
+    const size_t srow = (size_t)hq * D;
 
-    if (cnt <= MERGE_MAX_SLOTS) {
-        for (int i = tid; i < cnt; i += NT) sl[i] = slr[i];
-        __syncthreads();
-        for (int i = tid; i < cnt * MH; i += NT) {
-            const int s = i / MH, j = i - s * MH;
-            w[i] = j < nh ? lse[(size_t)sl[s] * hq + h0 + j] : NEG_INF;
-        }
-        __syncthreads();
-        if (tid < MH) {
-            float M = NEG_INF;
-            for (int s = 0; s < cnt; ++s) M = fmaxf(M, w[s * MH + tid]);
-            float Z = 0.f;
-            if (M != NEG_INF)
-                for (int s = 0; s < cnt; ++s) Z += fast_exp2((w[s * MH + tid] - M) * 1.44269504088896341f);
-            mh[tid] = M;
-            invz[tid] = Z > 0.f ? 1.f / Z : 0.f;
-        }
-        __syncthreads();
-        for (int i = tid; i < cnt * MH; i += NT) {
-            const int j = i % MH;
-            w[i] = mh[j] != NEG_INF ? fast_exp2((w[i] - mh[j]) * 1.44269504088896341f) * invz[j] : 0.f;
-        }
-        __syncthreads();
-        if (hl < nh) {
-            const float *src = part + (size_t)head * D + 4 * d4;
-            const size_t srow = (size_t)hq * D;
-            int s = 0;
-            for (; s + 8 <= cnt; s += 8) {
-                f32x4 v[8];
+    float M = NEG_INF, Z = 0.f;  // running max (log2 units) and weight sum
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < cnt; s0 += MERGE_CHUNK) {
+        float l[MERGE_CHUNK];
+        f32x4 v[MERGE_CHUNK];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) v[u] = *(const f32x4 *)(src + sl[s + u] * srow);
-#pragma unroll
-                for (int u = 0; u < 8; ++u) acc += w[(s + u) * MH + hl] * v[u];
-            }
-            for (; s < cnt; ++s) acc += w[s * MH + hl] * *(const f32x4 *)(src + sl[s] * srow);
+        for (int u = 0; u < MERGE_CHUNK; ++u) {
+            const int sl = slr[min(s0 + u, cnt - 1)];
+            l[u] = s0 + u < cnt ? lse[(size_t)sl * hq + head] * LOG2E : NEG_INF;
+            v[u] = *(const f32x4 *)(src + sl * srow);
         }
-    } else if (hl < nh) {
-        // many slots: two passes straight from global memory
-        float M = NEG_INF;
-        for (int s = 0; s < cnt; ++s) M = fmaxf(M, lse[(size_t)slr[s] * hq + head]);
-        if (M != NEG_INF) {
-            float Z = 0.f;
-            for (int s = 0; s < cnt; ++s) {
-                const size_t prow = (size_t)slr[s] * hq + head;
-                const float wt = fast_exp2((lse[prow] - M) * 1.44269504088896341f);
-                Z += wt;
-                acc += wt * *(const f32x4 *)(part + prow * D + 4 * d4);
-            }
-            acc *= 1.f / Z;
+        float cm = M;
+#pragma unroll
+        for (int u = 0; u < MERGE_CHUNK; ++u) cm = fmaxf(cm, l[u]);
+        if (cm == NEG_INF) continue;  // every slot so far is empty
+        if (cm > M) {
+            const float alpha = fast_exp2(M - cm);  // 0 while M is -inf
+            Z *= alpha;
+            acc *= alpha;
+            M = cm;
+        }
+#pragma unroll
+        for (int u = 0; u < MERGE_CHUNK; ++u) {
+            const float w = fast_exp2(l[u] - M);  // 0 for empty slots
+            Z += w;
+            acc += w * v[u];
         }
     }
-    if (hl < nh) {
-        u16 *dst = out + ((size_t)r * hq + head) * D + 4 * d4;
-        const u32x2 packed = {Ops<FP16>::pack(acc[0], acc[1]), Ops<FP16>::pack(acc[2], acc[3])};
-        *(u32x2 *)dst = packed;
-    }
+    if (Z > 0.f) acc *= 1.f / Z;
+    u16 *dst = out + ((size_t)r * hq + head) * D + 4 * d4;
+    *(u32x2 *)dst = u32x2{Ops<FP16>::pack(acc[0], acc[1]), Ops<FP16>::pack(acc[2], acc[3])};
 }
 
 // ------------------------------------------------------------------ launch
@@ -528,7 +501,7 @@ template <int D, bool FP16>
 hipError_t launch_segment(const SegParams &sp, int kind, hipStream_t stream) {
     if (sp.n_items <= 0) return hipSuccess;
 #ifndef TA_LEGACY_LARGE
-    if (kind != TA_SMALL) {
+    {
         // LDS-transpose kernels (segment_tile.hip) whenever the pool layout allows them
         const hipError_t e = launch_tile(sp, kind, D, FP16, stream);
         if (e != hipErrorNotSupported) return e;
@@ -536,8 +509,7 @@ hipError_t launch_segment(const SegParams &sp, int kind, hipStream_t stream) {
 #endif
     switch (kind) {
         case TA_SMALL: {
-            const long total = (long)sp.n_items * sp.hk;
-            const int blocks = (int)(total < SMALL_MAX_BLOCKS ? total : SMALL_MAX_BLOCKS);
+            const int blocks = sp.n_items < SMALL_MAX_BLOCKS ? sp.n_items : SMALL_MAX_BLOCKS;
             hipLaunchKernelGGL((seg_small_kernel<D, FP16>), dim3(blocks), dim3(SMALL_NT), 0, stream, sp);
             break;
         }

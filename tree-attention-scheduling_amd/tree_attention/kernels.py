@@ -19,9 +19,9 @@ Internal layout (the build's own; only ``out`` is contractual):
   ``lse [NSLOT, HQ]``; ``slots[r]`` lists request ``r``'s partial rows in job
   order (the reference instead indexes ``job * MAXR + local``, which allocates
   ``J * MAXR`` rows).
-* Work items: small jobs (<= 16 query rows) are processed one workgroup per
-  (job, KV head); larger jobs are cut into 64/128/256-row tiles, one
-  workgroup per (job, tile, KV head).
+* Work items are ``(job, first row, KV head)`` triples: small jobs (<= 16
+  query rows) get one per KV head, processed by one wave each; larger jobs
+  are cut into 64/128/256-row tiles, one workgroup per (job, tile, KV head).
 """
 from __future__ import annotations
 
@@ -70,20 +70,23 @@ class PreparedPlan:
 
 
 def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256):
-    """Work items per kernel kind as int32 arrays (see module docstring)."""
-    small = np.arange(small_jobs, dtype=np.int32)
-    large = {k: [] for k in _native.KIND_ROWS}
-    for j in range(small_jobs, len(jobs)):
+    """Work-item triples ``(job, first row, KV head)`` per kernel kind as int32 arrays.
+
+    Small jobs (<= 16 query rows) get one item per KV head; larger jobs one per
+    (row tile, KV head), the tile size chosen by ``_large_kind``.
+    """
+    triples = {k: [] for k in (_native.TA_SMALL, *_native.KIND_ROWS)}
+    for j in range(len(jobs)):
         rows = len(jobs[j].requests) * group
+        if j < small_jobs:
+            triples[_native.TA_SMALL].extend((j, 0, h) for h in range(kvheads))
+            continue
         kind = _large_kind(rows, tile_rows)
         tile = _native.KIND_ROWS[kind]
         for h in range(kvheads):
             for row0 in range(0, rows, tile):
-                large[kind].append((j, row0, h))
-    items = {_native.TA_SMALL: small}
-    for kind, triples in large.items():
-        items[kind] = np.asarray(triples, dtype=np.int32).reshape(-1)
-    return items
+                triples[kind].append((j, row0, h))
+    return {k: np.asarray(v, dtype=np.int32).reshape(-1) for k, v in triples.items()}
 
 
 def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256) -> PreparedPlan:
@@ -161,8 +164,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256) -> PreparedPlan:
     abi.rowbase, abi.slots, abi.counts = rowbase_t.data_ptr(), slots_t.data_ptr(), counts_t.data_ptr()
     for kind, view in item_views.items():
         abi.items[kind] = view.data_ptr() if view.numel() else None
-        per = 1 if kind == _native.TA_SMALL else 3
-        abi.n_items[kind] = view.numel() // per
+        abi.n_items[kind] = view.numel() // 3
     abi.part, abi.lse = part.data_ptr(), lse.data_ptr()
     abi.njobs, abi.maxr, abi.maxs, abi.nreq, abi.nslot = njobs, maxr, maxs, nreq, nslot
     abi.hq, abi.hk, abi.d = hq, kvheads, dim
