@@ -12,6 +12,8 @@ cost models, the full job list (requests and token runs, in order), the
 Tree specs are stored with the fixtures, so the tests rebuild every tree with
 the build's own ``KVTree`` and compare plans field by field.
 """
+import hashlib
+import itertools
 import json
 import random
 import sys
@@ -23,6 +25,10 @@ sys.path.insert(0, str(REF / "src"))
 from tree_attention import KVTree, CostModel, schedule  # noqa: E402  (reference package)
 
 METHODS = ("request", "fixed", "greedy", "cube")
+# the cost model fitted on MI355X (tree_attention.calibrate); plans under it must
+# match the reference planner too
+FITTED = json.loads((Path(__file__).resolve().parents[2] / "tree-attention-scheduling_amd" / "tree_attention"
+                     / "mi355x_cost_model.json").read_text())["params"]
 MI355X_LIKE = [
     dict(bandwidth=5.0e6, cube_flops=1.0e9, task_us=0.5, merge_us=0.01, cube_rows=16, key_tile=64,
          kv_split=256, max_query_rows=512),
@@ -60,6 +66,29 @@ def nested_unequal():
     return parents, lengths, leaves + [1, leaves[0], leaves[1]]
 
 
+def grid_tree(requests, context, fraction, depth):
+    """Balanced binary split of the shared region (same construction as tree_attention.shapes.grid_tree)."""
+    shared = int(fraction * context + 0.5)
+    private = context - shared
+    level_len = [shared // depth + (1 if i < shared % depth else 0) for i in range(depth)]
+    parents, lengths = [-1], [level_len[0]]
+    level = [0]
+    for i in range(1, depth):
+        nxt = []
+        for parent in level:
+            for _ in range(2):
+                nxt.append(len(parents))
+                parents.append(parent)
+                lengths.append(level_len[i])
+        level = nxt
+    terminals = []
+    for r in range(requests):
+        terminals.append(len(parents))
+        parents.append(level[r * len(level) // requests])
+        lengths.append(private)
+    return parents, lengths, terminals
+
+
 def random_tree(rng):
     n = rng.randint(2, 12)
     parents, lengths = [-1], [rng.choice([0, 1, 7, 48, 300, 700, 1500])]
@@ -73,12 +102,17 @@ def random_tree(rng):
     return parents, lengths, terminals
 
 
-def plan_record(tree, method, heads, model_kw):
+def plan_record(tree, method, heads, model_kw, digest=False):
     model = CostModel(**model_kw)
     plan = schedule(tree, heads[0], heads[1], heads[2], method, model)
-    return {"method": method, "heads": list(heads), "model": model_kw,
-            "estimated_us": plan.estimated_us,
-            "jobs": [[list(j.requests), runs(j.tokens)] for j in plan.jobs]}
+    jobs = [[list(j.requests), runs(j.tokens)] for j in plan.jobs]
+    rec = {"method": method, "heads": list(heads), "model": model_kw, "estimated_us": plan.estimated_us}
+    if digest:  # large plans: the exact job list, as a SHA-256 of its canonical JSON
+        rec["njobs"] = len(jobs)
+        rec["jobs_sha256"] = hashlib.sha256(json.dumps(jobs, separators=(",", ":")).encode()).hexdigest()
+    else:
+        rec["jobs"] = jobs
+    return rec
 
 
 def tree_record(tree):
@@ -91,12 +125,14 @@ def tree_record(tree):
 def main():
     cases = []
 
-    def add(name, kind, spec, heads=(32, 8, 128), models=({},), methods=METHODS):
+    def add(name, kind, spec, heads=(32, 8, 128), models=({},), methods=METHODS, digest=False):
         tree = KVTree.synthetic(*spec) if kind == "synthetic" else KVTree.from_sequences(spec)
-        case = {"name": name, "kind": kind, "spec": spec, "tree": tree_record(tree), "plans": []}
+        case = {"name": name, "kind": kind, "spec": spec, "plans": []}
+        if not digest:
+            case["tree"] = tree_record(tree)
         for model_kw in models:
             for method in methods:
-                case["plans"].append(plan_record(tree, method, heads, model_kw))
+                case["plans"].append(plan_record(tree, method, heads, model_kw, digest))
         cases.append(case)
 
     bench = {
@@ -108,9 +144,14 @@ def main():
         "no_share_long": shared_prefix(128, 0, 8192),
     }
     for name, spec in bench.items():
-        add(name, "synthetic", spec, models=({},) + tuple(MI355X_LIKE) if name == "wide_long" else ({},))
-    add("cpu_baseline", "synthetic", shared_prefix(8, 1024, 64))
-    add("nested_unequal", "synthetic", nested_unequal(), models=({},) + tuple(MI355X_LIKE))
+        add(name, "synthetic", spec, models=({}, FITTED) + tuple(MI355X_LIKE) if name == "wide_long" else ({}, FITTED))
+    add("cpu_baseline", "synthetic", shared_prefix(8, 1024, 64), models=({}, FITTED))
+    add("nested_unequal", "synthetic", nested_unequal(), models=({}, FITTED) + tuple(MI355X_LIKE))
+    # the 81-shape requests x context x shared-fraction x depth grid, fitted model
+    for requests, context, fraction, depth in itertools.product((16, 32, 128), (1024, 4096, 8192),
+                                                                (0.25, 0.75, 0.99), (1, 2, 3)):
+        add(f"grid_{requests}_{context}_{fraction}_{depth}", "synthetic",
+            grid_tree(requests, context, fraction, depth), models=(FITTED,), digest=True)
     # tests/test_semantics.py trees, CostModel(kv_split=48), 8 Q / 2 KV heads, d = 32
     for name, kind, spec in (
             ("semantics_unequal", "sequences", [[1, 2, 3], [1, 2], [1, 2, 4, 5, 6], [7, 8], [1, 2, 3]]),
@@ -126,7 +167,7 @@ def main():
         add(name, kind, spec, heads=(8, 2, 64), models=({"kv_split": 128},))
     workloads = json.loads((REF / "configs/qwen_workloads.json").read_text())["workloads"]
     for name, seqs in workloads.items():
-        add(f"qwen_{name}", "sequences", seqs, models=({}, MI355X_LIKE[0]))
+        add(f"qwen_{name}", "sequences", seqs, models=({}, MI355X_LIKE[0], FITTED))
     rng = random.Random(20261201)
     made = 0
     while made < 40:
@@ -136,7 +177,7 @@ def main():
         except ValueError:  # a request whose whole path has no tokens
             continue
         add(f"random_{made}", "synthetic", spec, models=({}, {"kv_split": 64, "max_query_rows": 16},
-                                                         MI355X_LIKE[made % 2]))
+                                                         MI355X_LIKE[made % 2], FITTED))
         made += 1
     OUT.write_text(json.dumps({"source": "reference src/tree_attention/{tree,schedule}.py", "cases": cases},
                               separators=(",", ":")))

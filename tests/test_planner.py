@@ -5,6 +5,7 @@ job counts) and by plans the reference implementation produced for the same
 trees and cost parameters (tests/golden/make_plan_fixtures.py).
 """
 import gc
+import hashlib
 import json
 import weakref
 from pathlib import Path
@@ -101,12 +102,17 @@ def test_plans_match_reference_implementation():
             q, k, d = want["heads"]
             plan = schedule(tree, q, k, d, want["method"], CostModel(**want["model"]))
             got = [[list(j.requests), _runs(j.tokens)] for j in plan.jobs]
-            assert got == want["jobs"], (case["name"], want["method"], want["model"])
+            if "jobs" in want:
+                assert got == want["jobs"], (case["name"], want["method"], want["model"])
+            else:  # large plans are stored as a digest of the same canonical JSON
+                assert len(got) == want["njobs"], (case["name"], want["method"])
+                digest = hashlib.sha256(json.dumps(got, separators=(",", ":")).encode()).hexdigest()
+                assert digest == want["jobs_sha256"], (case["name"], want["method"], want["model"])
             assert plan.estimated_us == want["estimated_us"], (case["name"], want["method"], want["model"])
             assert plan.settings == {**CostModel(**want["model"]).__dict__, "qheads": q, "kvheads": k,
                                      "head_dim": d}
             n += 1
-    assert n > 400
+    assert n > 900
 
 
 def test_dynamic_plan_not_worse_than_greedy():

@@ -8,18 +8,32 @@ from tree_attention.kernels import CachedDecodePlan, prepare
 from tree_attention.schedule import Job, Plan
 
 
+def _covers_paths(prepared, tree):
+    """Every request's execution jobs cover its path exactly once."""
+    seen = [[] for _ in tree.paths]
+    for job in prepared.jobs:
+        for r in job.requests:
+            seen[r].extend(job.tokens)
+    return all(sorted(seen[r]) == sorted(path) for r, path in enumerate(tree.paths))
+
+
 def test_metadata_layout_small_first_and_compact_slots():
     tree = shapes.tree(shapes.headline())
     q = torch.empty(128, 32, 128, dtype=torch.bfloat16)
     p = prepare(schedule(tree, 32, 8, 128, "cube"), q)
-    assert len(p.jobs) == 256 and p.small_jobs == 128
-    assert all(len(j.requests) == 1 for j in p.jobs[:128])
+    # default model: 16-request groups x 512-token chunks of the root; each group's
+    # chunks are re-cut into 4 chunks of 2032 tokens (8 groups x 4 x 8 heads = 256
+    # one-tile workgroups), the 128 private tails stay small jobs
+    assert p.small_jobs == 128 and len(p.jobs) == 128 + 32
+    assert all(len(j.requests) == 1 and len(j.tokens) == 64 for j in p.jobs[:128])
+    assert all(len(j.requests) == 16 and len(j.tokens) == 2032 for j in p.jobs[128:])
+    assert _covers_paths(p, tree)
     assert p.contiguous_k
     qlen = p.qlen.tolist()
     rowbase = p.rowbase.tolist()
     assert rowbase == [sum(qlen[:i]) for i in range(len(qlen))]
     counts = p.counts.tolist()
-    assert counts == [17] * 128
+    assert counts == [5] * 128
     # every request's slots point at rows of jobs that contain it
     slot_owner = {}
     for j, job in enumerate(p.jobs):
@@ -28,13 +42,37 @@ def test_metadata_layout_small_first_and_compact_slots():
     for r in range(128):
         assert {slot_owner[s] for s in p.slots[r, :counts[r]].tolist()} == {r}
     assert p.part.shape == (sum(qlen), 32, 128) and p.lse.shape == (sum(qlen), 32)
-    # work items: 128 small jobs; large jobs of 16 requests = 64 rows -> one 64-row tile per head
+    # work items: one per (small job, head); large jobs of 16 requests = 64 rows -> one 64-row tile per head
     assert p.abi.n_items[_native.TA_SMALL] == 128 * 8
     small = p.items[_native.TA_SMALL].view(-1, 3).tolist()
     assert sorted(small) == [[j, 0, h] for j in range(128) for h in range(8)]
-    assert p.abi.n_items[_native.TA_LARGE64] == 128 * 8
+    assert p.abi.n_items[_native.TA_LARGE64] == 32 * 8
     items = p.items[_native.TA_LARGE64].view(-1, 3).tolist()
-    assert sorted(set((j, h) for j, _, h in items)) == [(j, h) for j in range(128, 256) for h in range(8)]
+    assert sorted(set((j, h) for j, _, h in items)) == [(j, h) for j in range(128, 160) for h in range(8)]
+
+
+def test_recut_is_independent_of_the_plans_kv_split():
+    """The GPU work split depends on the request groups, not on where the plan cut them."""
+    tree = shapes.tree(shapes.headline())
+    q = torch.empty(128, 32, 128, dtype=torch.bfloat16)
+    splits = []
+    for kv_split in (128, 256, 512, 8192):
+        p = prepare(schedule(tree, 32, 8, 128, "cube", CostModel(kv_split=kv_split, max_query_rows=512)), q)
+        assert _covers_paths(p, tree)
+        splits.append([(j.requests, j.tokens[0], len(j.tokens)) for j in p.jobs])
+    assert all(s == splits[0] for s in splits[1:])
+    # 16 root chunks (512 rows = 2 tiles x 8 heads = 16 workgroups each): 256 workgroups
+    assert sum(len(r) == 128 for r, _, _ in splits[0]) == 16
+
+
+def test_recut_keeps_cached_tails_fixed():
+    tree = shapes.tree(shapes.shared_prefix(4, 100, 20))
+    prefix = tree.storage_tokens
+    q = torch.empty(4, 32, 32, dtype=torch.float16)
+    cached = CachedDecodePlan(schedule(tree, 32, 2, 32, "request", CostModel(kv_split=16)), q, prefix, 6)
+    tails = [cached.prepared.jobs[i] for i in cached.tail_indices.tolist()]
+    assert sorted((j.requests, j.tokens[0], len(j.tokens)) for j in tails) == [
+        ((r,), prefix + 6 * r, 6) for r in range(4)]
 
 
 def test_large_row_tiles():
@@ -44,7 +82,9 @@ def test_large_row_tiles():
     p = prepare(schedule(tree, 32, 8, 128, "cube", model), q)
     n256 = p.abi.n_items[_native.TA_LARGE256]
     big = [j for j in p.jobs if len(j.requests) == 128]
-    assert len(big) == 32 and n256 == 32 * 8 * 2
+    assert len(big) == 16 and n256 == 16 * 8 * 2
+    p = prepare(schedule(tree, 32, 8, 128, "cube", model), q, tile_rows=128)
+    assert p.abi.n_items[_native.TA_LARGE128] == 8 * 8 * 4  # 4 row tiles: 8 chunks fill the GPU
 
 
 def test_rejects_bad_jobs():

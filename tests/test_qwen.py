@@ -86,7 +86,8 @@ def test_pool_layout_and_capacity_cpu(monkeypatch):
     assert tree.storage_tokens == 12 and decoder.prefix_size == 12
     assert decoder.capacity == 12 + 4 * 2
     kp, vp = decoder.pools[0]
-    assert kp.shape == (2, 32, decoder.capacity) and vp.shape == (2, decoder.capacity, 32)
+    alloc = (decoder.capacity + 7) // 8 * 8
+    assert kp.shape == (2, 32, alloc) and vp.shape == (2, alloc, 32)
     monkeypatch.setattr(integration, "attention_matrix", OracleAttention(decoder))
     decoder.step([0, 1, 2, 3])
     decoder.step([4, 5, 6, 7])

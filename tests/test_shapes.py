@@ -1,0 +1,57 @@
+"""Evaluation and calibration tree shapes (tree_attention.shapes)."""
+from tree_attention import shapes
+
+
+def _lengths_and_requests(spec):
+    parents, lengths, terminals = spec
+    return {n for n in lengths if n}, {len(terminals)}
+
+
+def _evaluation_specs():
+    specs = [shapes.headline(), shapes.cpu_baseline_shape(), shapes.nested_unequal()]
+    specs += list(shapes.benchmark_cases().values())
+    specs += [s for _, s in shapes.reference_grid()]
+    specs += [s for _, s in shapes.config_grid()]
+    return specs
+
+
+def test_calibration_grid_is_disjoint_from_evaluation_shapes():
+    """The MI355X cost model is fitted on shapes that no evaluation uses."""
+    cal_len, cal_req = set(), set()
+    for _, spec in shapes.calibration_grid():
+        lengths, reqs = _lengths_and_requests(spec)
+        cal_len |= lengths
+        cal_req |= reqs
+    ev_len, ev_req = set(), set()
+    for spec in _evaluation_specs():
+        lengths, reqs = _lengths_and_requests(spec)
+        ev_len |= lengths
+        ev_req |= reqs
+    assert not cal_len & ev_len
+    assert not cal_req & ev_req
+
+
+def test_headline_and_nested_shapes():
+    t = shapes.tree(shapes.headline())
+    assert t.storage_tokens == 16_320
+    assert sum(map(len, t.paths)) == 1_048_576
+    n = shapes.tree(shapes.nested_unequal())
+    assert n.storage_tokens == 20_480 and len(n.paths) == 35
+    assert len(n.paths[32]) == 4096 + 1024          # terminates at an internal node
+    assert n.paths[33] == n.paths[0] and n.paths[34] == n.paths[1]  # duplicates
+
+
+def test_config_grid_is_a_full_factorial():
+    rows = list(shapes.config_grid())
+    assert len(rows) == 81
+    for params, spec in rows:
+        t = shapes.tree(spec)
+        assert len(t.paths) == params["requests"]
+        assert all(len(p) == params["context"] for p in t.paths)
+        shared = int(params["fraction"] * params["context"] + 0.5)
+        # every request shares exactly the `shared` prefix of the root chain with request 0's subtree
+        leaves = 2 ** (params["depth"] - 1)
+        assert t.storage_tokens == sum(
+            (2 ** i) * (shared // params["depth"] + (1 if i < shared % params["depth"] else 0))
+            for i in range(params["depth"])) + params["requests"] * (params["context"] - shared)
+        assert leaves <= params["requests"]

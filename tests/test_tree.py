@@ -72,6 +72,8 @@ def test_node_structure_matches_reference():
     data = json.loads((GOLDEN / "plan_fixtures.json").read_text())
     checked = 0
     for case in data["cases"]:
+        if "tree" not in case:  # digest-only plan cases
+            continue
         if case["kind"] == "sequences":
             tree = KVTree.from_sequences(case["spec"])
         else:

@@ -1,0 +1,183 @@
+"""Fit the MI355X cost-model terms from measured attention layers.
+
+    python -m tree_attention.calibrate [--out PATH] [--iters 20]
+
+The reference fits its ``CostModel`` (schedule.py:29-52) for Ascend 910B from
+tile sweeps on two calibration trees (scripts/calibrate_tiles.py:13-22).  Here
+the same formula is kept and only its parameters are refitted on one MI355X:
+
+* ``cube_rows`` (16) and ``key_tile`` (64) are the kernels' own constants: jobs
+  of at most 16 query rows run on the one-wave small-job path, K/V are staged
+  in 64-token tiles and large jobs step through them 32 tokens at a time
+  (``key_tile // 2``).
+* ``kv_split`` and ``max_query_rows`` are structural: for every candidate pair
+  the continuous terms are fitted and the pair whose subset-DP (``cube``) plans
+  measure fastest on the calibration grid (geometric mean over its trees) is
+  kept.
+* ``bandwidth``, ``cube_flops``, ``task_us`` and ``merge_us`` are fitted by
+  least squares on log((launch + estimated_us) / measured_us) over every plan
+  of every method on the calibration grid, with the layer's fixed launch cost
+  as a nuisance term that the planner does not use.  Plans of ``greedy`` / ``cube`` depend on the
+  parameters, so the fit is repeated with plans re-made from the fitted values.
+
+The calibration trees (``shapes.calibration_grid``) share no request count or
+segment length with any evaluation shape.  The fitted parameters are written
+to ``mi355x_cost_model.json`` next to this module, together with the fit
+residuals and the command that produced them.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import sys
+import time
+from dataclasses import asdict
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import shapes
+from .kernels import attention_matrix, pack_kv, prepare
+from .schedule import CostModel, physical_jobs, schedule
+
+METHODS = ("request", "fixed", "greedy", "cube")
+HQ, HK, D = 32, 8, 128
+FIT_FIELDS = ("bandwidth", "cube_flops", "task_us", "merge_us")
+OUT = Path(__file__).with_name("mi355x_cost_model.json")
+
+
+def _features(plan):
+    """Per-physical-job (nreq, ntok) pairs of a plan, in job order."""
+    return [(len(j.requests), len(j.tokens)) for j in physical_jobs(plan.jobs)]
+
+
+def _estimate(feats, model: CostModel) -> float:
+    total = 0.0
+    for nreq, ntok in feats:
+        total += model._cost_n(nreq, ntok, HQ, HK, D)
+    return total
+
+
+class Bench:
+    """Device inputs of one tree and a timer for its plans."""
+
+    def __init__(self, tree, dev, pools=3, seed=11):
+        g = torch.Generator().manual_seed(seed)
+        t = tree.storage_tokens
+        t8 = (t + 7) // 8 * 8  # an 8-aligned pool, as the model's pools are
+        self.tree = tree
+        self.q = torch.randn(len(tree.paths), HQ, D, generator=g).bfloat16().to(dev)
+        k = torch.randn(t8, HK, D, generator=g).bfloat16().to(dev)
+        v = torch.randn(t8, HK, D, generator=g).bfloat16().to(dev)
+        kp, vp = pack_kv(k, v)
+        self.pools = [(kp, vp)] + [(kp.clone(), vp.clone()) for _ in range(pools - 1)]
+
+    def time_plan(self, plan, iters: int) -> float:
+        prepared = prepare(plan, self.q)
+        for i in range(3):
+            attention_matrix(self.q, *self.pools[i % len(self.pools)], prepared)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(iters):
+            attention_matrix(self.q, *self.pools[i % len(self.pools)], prepared)
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e3 / iters
+
+
+def fit_terms(samples, model: CostModel):
+    """Least-squares fit of the continuous terms on log((launch + estimate) / measured).
+
+    ``launch`` -- the fixed cost of one layer's kernel launches, which every plan
+    pays alike -- is fitted alongside as a nuisance term; the planner's formula
+    has no such term and compares plans without it.  Returns (model, launch_us).
+    """
+    from scipy.optimize import least_squares
+
+    x0 = np.log([getattr(model, f) for f in FIT_FIELDS] + [5.0])
+
+    def unpack(x):
+        e = np.exp(x)
+        return CostModel(**{**asdict(model), **dict(zip(FIT_FIELDS, map(float, e[:4])))}), float(e[4])
+
+    def residual(x):
+        m, launch = unpack(x)
+        return np.array([math.log((launch + _estimate(f, m)) / t) for f, t in samples])
+
+    # 0.1-20 TB/s, 0.1-10 PFLOP/s, 1 ns-100 us per task, 0.1 ns-10 us per merged request, 0.1-100 us launch
+    lo = np.log([1e5, 1e8, 1e-3, 1e-4, 1e-1])
+    hi = np.log([2e7, 1e10, 1e2, 1e1, 1e2])
+    res = least_squares(residual, np.clip(x0, lo + 1e-9, hi - 1e-9), bounds=(lo, hi), method="trf")
+    return unpack(res.x)
+
+
+def calibrate(iters=20, kv_splits=(256, 512, 1024), query_rows=(64, 128, 256, 512), log=print):
+    dev = torch.device("cuda:0")
+    benches = [(name, Bench(shapes.tree(spec), dev)) for name, spec in shapes.calibration_grid()]
+    start = CostModel(bandwidth=5.0e6, cube_flops=1.0e9, task_us=0.5, merge_us=0.01, cube_rows=16,
+                      key_tile=64)
+    measured = {}
+
+    def measure(bench_name, bench, plan):
+        key = (bench_name, tuple((j.requests, j.tokens) for j in plan.jobs))
+        if key not in measured:
+            measured[key] = bench.time_plan(plan, iters)
+        return measured[key]
+
+    candidates = []
+    for kv_split in kv_splits:
+        for mqr in query_rows:
+            model = CostModel(**{**asdict(start), "kv_split": kv_split, "max_query_rows": mqr})
+            samples = []
+            for _round in range(2):
+                for name, b in benches:
+                    for method in METHODS:
+                        plan = schedule(b.tree, HQ, HK, D, method, model)
+                        samples.append((_features(plan), measure(name, b, plan)))
+                model, launch = fit_terms(samples, model)
+            cube = {name: measure(name, b, schedule(b.tree, HQ, HK, D, "cube", model)) for name, b in benches}
+            req = {name: measure(name, b, schedule(b.tree, HQ, HK, D, "request", model)) for name, b in benches}
+            cube_us, req_us = sum(cube.values()), sum(req.values())
+            err = [math.log((launch + _estimate(f, model)) / t) for f, t in samples]
+            row = {"params": asdict(model), "launch_us": launch, "cube_total_us": cube_us,
+                   "request_total_us": req_us,
+                   "cube_geomean_us": float(np.exp(np.mean(np.log(list(cube.values()))))),
+                   "cube_us": cube, "fit_rms_log_error": float(np.sqrt(np.mean(np.square(err)))),
+                   "samples": len(samples)}
+            candidates.append(row)
+            log(json.dumps(row))
+    # every calibration tree counts alike: geometric mean of the cube plans' times
+    best = min(candidates, key=lambda r: r["cube_geomean_us"])
+    return best, candidates
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--out", default=str(OUT))
+    ap.add_argument("--iters", type=int, default=20)
+    args = ap.parse_args(argv)
+    t0 = time.time()
+    best, candidates = calibrate(iters=args.iters, log=lambda s: print(s, flush=True))
+    doc = {
+        "status": "fitted on one MI355X",
+        "command": "python -m tree_attention.calibrate " + " ".join(argv or sys.argv[1:]),
+        "device": torch.cuda.get_device_name(0),
+        "calibration_grid": [name for name, _ in shapes.calibration_grid()],
+        "params": best["params"],
+        "launch_us": best["launch_us"],
+        "fit_rms_log_error": best["fit_rms_log_error"],
+        "cube_total_us": best["cube_total_us"],
+        "cube_geomean_us": best["cube_geomean_us"],
+        "request_total_us": best["request_total_us"],
+        "candidates": candidates,
+        "seconds": round(time.time() - t0, 1),
+    }
+    Path(args.out).write_text(json.dumps(doc, indent=1) + "\n")
+    print(json.dumps({"best": best["params"], "out": args.out}), flush=True)
+
+
+if __name__ == "__main__":
+    main()

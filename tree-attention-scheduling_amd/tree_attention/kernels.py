@@ -11,9 +11,10 @@ PyTorch fallback: without the library every call raises ``RuntimeError``.
 Internal layout (the build's own; only ``out`` is contractual):
 
 * ``qids [J, MAXR]``, ``kids [J, 1]`` (first physical token), ``qlen [J]``,
-  ``klen [J]`` as in the reference (kernels.py:114-128); jobs are the plan's
-  physical jobs, stably sorted small-first exactly like the reference
-  (kernels.py:109-110) so ``CachedDecodePlan.tail_indices`` match.
+  ``klen [J]`` as in the reference (kernels.py:114-128), over execution jobs:
+  the plan's physical jobs, small ones (<= 16 query rows) first as in the
+  reference (kernels.py:109-110), with runs of jobs over one request group
+  re-cut into chunks sized for the GPU (``_recut``).
 * Partial outputs are compact: job ``j``'s requests own partial rows
   ``rowbase[j] .. rowbase[j] + qlen[j]`` of ``part [NSLOT, HQ, D]`` and
   ``lse [NSLOT, HQ]``; ``slots[r]`` lists request ``r``'s partial rows in job
@@ -89,13 +90,65 @@ def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256):
     return {k: np.asarray(v, dtype=np.int32).reshape(-1) for k, v in triples.items()}
 
 
-def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256) -> PreparedPlan:
+TOKEN_QUANTUM = 64  # tokens per LDS tile of the segment kernels
+
+
+def _recut(jobs, items_per_chunk, target_items, fixed_from):
+    """Execution jobs for one kernel kind: runs of consecutive jobs over the same
+    requests and contiguous tokens are cut again into near-equal chunks, as long
+    as possible while the kind still gets ``target_items`` work items (one
+    workgroup per CU for the large kinds).  Fewer, longer chunks mean fewer
+    partial outputs to write and merge; the result is the same attention.
+    Jobs whose tokens start at or after ``fixed_from`` (growing decode tails)
+    are left alone.
+    """
+    runs = []  # [requests, first token, length, fixed]
+    for job in jobs:
+        t0, n = job.tokens[0], len(job.tokens)
+        fixed = fixed_from is not None and t0 >= fixed_from
+        last = runs[-1] if runs else None
+        if last and not fixed and not last[3] and last[0] == job.requests and last[1] + last[2] == t0:
+            last[2] += n
+        else:
+            runs.append([job.requests, t0, n, fixed])
+
+    def count(limit):
+        return sum(items_per_chunk(r) * (1 if f else -(-n // limit)) for r, _, n, f in runs)
+
+    longest = max((n for _, _, n, f in runs if not f), default=0)
+    if longest == 0:
+        return jobs
+    limit = -(-longest // TOKEN_QUANTUM) * TOKEN_QUANTUM
+    while limit > TOKEN_QUANTUM and count(limit) < target_items:
+        limit -= TOKEN_QUANTUM
+    out = []
+    for reqs, t0, n, fixed in runs:
+        if fixed:
+            out.append(Job(reqs, tuple(range(t0, t0 + n))))
+            continue
+        pieces = -(-n // limit)
+        size = -(-(-(-n // pieces)) // 8) * 8  # near-equal, 8-token aligned
+        for a in range(0, n, size):
+            out.append(Job(reqs, tuple(range(t0 + a, t0 + min(n, a + size)))))
+    return out
+
+
+def _cu_count(device) -> int:
+    if device.type == "cuda":
+        return torch.cuda.get_device_properties(device).multi_processor_count
+    return 256  # MI355X
+
+
+def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int | None = None) -> PreparedPlan:
     """Lower ``plan`` to device metadata and scratch for queries shaped like ``q``.
 
     Mirrors kernels.py:103-141: physical jobs, stable small-first order, one
     host-to-device copy of all int32 metadata, scratch allocated once.
     ``tile_rows`` (64, 128 or 256) caps the query rows one workgroup of the
-    large-job kernels handles; it changes the work split, not the result.  Raises
+    large-job kernels handles; it changes the work split, not the result.
+    Runs of jobs over one request group are re-cut for the GPU (``_recut``), so
+    ``jobs`` holds the execution jobs; ``fixed_from`` keeps jobs whose tokens
+    start at or after it (decode tails whose length changes) as they are.  Raises
     ``ValueError`` for jobs without requests or tokens, request ids outside
     ``q`` and token runs that are not consecutive physical ids.
     """
@@ -107,10 +160,22 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256) -> PreparedPlan:
         raise ValueError("Query heads must be divisible by KV heads")
     group = hq // kvheads
     jobs = physical_jobs(plan.jobs)
-    jobs.sort(key=lambda job: len(job.requests) * group > SMALL_ROWS)
-    small_jobs = sum(len(job.requests) * group <= SMALL_ROWS for job in jobs)
+    for i, job in enumerate(jobs):
+        toks = job.tokens
+        if not job.requests or not toks:
+            raise ValueError("Every job needs requests and tokens")
+        if toks[0] < 0 or (len(toks) > 1 and toks != tuple(range(toks[0], toks[0] + len(toks)))):
+            raise ValueError(f"Job {i} tokens are not one run of consecutive physical ids")
     if not jobs:
         raise ValueError("Plan has no jobs")
+    small = [j for j in jobs if len(j.requests) * group <= SMALL_ROWS]
+    large = [j for j in jobs if len(j.requests) * group > SMALL_ROWS]
+    n_cu = _cu_count(q.device)
+    small = _recut(small, lambda r: kvheads, 8 * n_cu, fixed_from)
+    large = _recut(large, lambda r: -(-len(r) * group // _native.KIND_ROWS[_large_kind(len(r) * group, tile_rows)])
+                   * kvheads, n_cu, fixed_from)
+    jobs = small + large
+    small_jobs = len(small)
     njobs = len(jobs)
     maxr = max(len(j.requests) for j in jobs)
     qids = np.zeros((njobs, maxr), dtype=np.int32)
@@ -122,11 +187,6 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256) -> PreparedPlan:
     nslot = 0
     for i, job in enumerate(jobs):
         reqs, toks = job.requests, job.tokens
-        if not reqs or not toks:
-            raise ValueError("Every job needs requests and tokens")
-        if toks[-1] - toks[0] + 1 != len(toks) or toks[0] < 0 or (
-                len(toks) > 1 and toks != tuple(range(toks[0], toks[0] + len(toks)))):
-            raise ValueError(f"Job {i} tokens are not one run of consecutive physical ids")
         qids[i, :len(reqs)] = reqs
         kids[i, 0] = toks[0]
         qlen[i] = len(reqs)
@@ -264,7 +324,7 @@ class CachedDecodePlan:
         plan = Plan(prefix_plan.jobs + tails, prefix_plan.method, prefix_plan.estimated_us,
                     prefix_plan.settings)
         self.max_new_tokens = max_new_tokens
-        self.prepared = prepare(plan, q)
+        self.prepared = prepare(plan, q, fixed_from=prefix_tokens)
         ordered = self.prepared.jobs
         self.tail_indices = torch.tensor([i for i, job in enumerate(ordered) if job.tokens[0] >= prefix_tokens],
                                          device=q.device)

@@ -70,8 +70,11 @@ class SharedKVDecoder:
         self.capacity = self.prefix_size + len(self.sequences) * max_new_tokens
         self.generated = 0
         dtype = model.dtype
-        self.pools = [(torch.empty((self.hk, self.dim, self.capacity), device=self.device, dtype=dtype),
-                       torch.empty((self.hk, self.capacity, self.dim), device=self.device, dtype=dtype))
+        # pools are allocated 8-token aligned (the kernels' fast path); positions
+        # past `capacity` are never written or read
+        alloc = (self.capacity + 7) // 8 * 8
+        self.pools = [(torch.empty((self.hk, self.dim, alloc), device=self.device, dtype=dtype),
+                       torch.empty((self.hk, alloc, self.dim), device=self.device, dtype=dtype))
                       for _ in model.model.layers]
         self.leaves = [_find_leaf(self.tree, r) for r in range(len(self.sequences))]
         self._prefill()

@@ -131,3 +131,11 @@ def calibration_grid():
     for requests in (6, 20, 40):
         for private in (700, 2000):
             yield f"private_r{requests}_{private}", shared_prefix(requests, 0, private)
+    # large shapes, where launch overheads are a small part of the layer
+    for requests, root, private in ((112, 7000, 50), (80, 6000, 150), (72, 3500, 90)):
+        yield f"shared_r{requests}_{root}_{private}", shared_prefix(requests, root, private)
+    parents, lengths = [-1, 0, 0], [2500, 1800, 2200]
+    for leaf in range(60):
+        parents.append(1 + leaf % 2)
+        lengths.append((73, 79, 91)[leaf % 3])
+    yield "two_level_r60", (parents, lengths, list(range(3, 63)))
