@@ -1,6 +1,6 @@
 """Benchmark: one decode-step tree-attention layer at 128 x 8192 (8128 shared) on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--method cube] [--no-graph]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--method cube]
 
 Workload: 128 requests, one 8128-token shared root plus 64 private tokens each
 (16,320 physical vs 1,048,576 logical KV positions), 32 query / 8 KV heads,
@@ -9,11 +9,21 @@ plan under the MI355X cost model.  One step = one ``attention_matrix`` call
 (segment kernels + merge) on resident pools.  Steps rotate over 8 distinct KV
 pools (535 MB, above the 256 MB MALL) so the bandwidth is HBM bandwidth.
 
-Timing: HIP events on the launch stream around exactly K steps after W
-warm-up steps, with a device synchronize on both sides.  By default the K
-steps are replays of a HIP graph that holds one layer per pool (launch gaps
-of the Python host loop removed); ``--no-graph`` times eager calls.  Graph
-replays are checked against eager results before timing.
+Timing: HIP events on the launch stream around exactly K eager steps after W
+warm-up steps, with a device synchronize on both sides.  The same layers are
+also replayed from a HIP graph (one layer per pool), checked against the
+eager results and reported as ``graph_us_per_layer``: on this path graph
+replay is slightly slower than back-to-back eager launches.  Per-kernel
+``kernel_us`` are the kernels' own durations (dispatch begin/end stamps of
+every launch through hipExtLaunchKernel events); ``kernel_graph_slot_us`` is
+each kernel's share of a graph of back-to-back launches, gaps included.  The
+roofline figure divides the dominant kernel's algorithmic work by its
+``kernel_us``.
+
+The CPU leg times the FP32 oracle (oracle/attention_oracle.py, the restatement
+of the reference's reference.py) on the host cores on the same layer, and is
+also the parity gate: the GPU output must be within 0.3% relative L2 of the
+oracle's per-request attention.
 
 Prints one JSON line (see the repository's bench contract).
 """
@@ -37,6 +47,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 R, HQ, HK, D = 128, 32, 8, 128
 SHARED, PRIVATE = 8128, 64
 POOLS = 8
+REL_L2_BOUND = 3e-3
 
 
 def parse():
@@ -46,7 +57,6 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--method", default="cube")
     ap.add_argument("--cost-model", default="mi355x", choices=["mi355x", "reference"])
-    ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     ap.add_argument("--seed", type=int, default=101)
     return ap.parse_args()
@@ -60,12 +70,12 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the attention path is single-device; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the attention path runs on one device)", file=sys.stderr)
         sys.exit(2)
     import torch
     from tree_attention import CostModel, schedule, shapes
     from tree_attention import _native
-    from tree_attention.kernels import attention_matrix, merge, pack_kv, prepare, segment
+    from tree_attention.kernels import attention_matrix, launch_durations_us, merge, pack_kv, prepare, segment
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -96,13 +106,15 @@ def main():
         kp, vp = pools[i % POOLS]
         return attention_matrix(qd, kp, vp, prepared)
 
-    # correctness gate (oracle on the host) before any timing
     eager = [layer(i).clone() for i in range(POOLS)]
     torch.cuda.synchronize()
-    from oracle.attention_oracle import relative_l2, request_attention
-    ref = request_attention(q.float(), k.float(), v.float(), tree)
-    rel = relative_l2(eager[0].cpu(), ref)
-    if rel > 3e-3 or not all(torch.equal(eager[0], e) for e in eager[1:]):
+    if not all(torch.equal(eager[0], e) for e in eager[1:]):
+        print(json.dumps({"error": "pools with equal contents gave different outputs"}), flush=True)
+        sys.exit(1)
+
+    # CPU leg first: the oracle on the host is also the parity gate before any timing
+    cpu, rel = cpu_baseline(q, k, v, tree, plan, eager[0].cpu(), args.cpu_budget_s)
+    if not rel <= REL_L2_BOUND:
         print(json.dumps({"error": "parity gate failed", "rel_l2": rel}), flush=True)
         sys.exit(1)
 
@@ -118,37 +130,46 @@ def main():
         torch.cuda.synchronize()
         return start.elapsed_time(end) * 1e3 / steps  # us per step
 
-    use_graph = not args.no_graph
-    if use_graph:
+    def capture(fn, n):
+        """A HIP graph of fn(0..n-1), captured on a side stream that the current stream joins."""
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         side.wait_stream(stream)
         with torch.cuda.stream(side):
-            layer(0)  # warm the side stream
+            fn(0)
         stream.wait_stream(side)
         outs = []
         with torch.cuda.graph(graph, stream=side):
-            for i in range(POOLS):
-                outs.append(layer(i).clone())
+            for i in range(n):
+                outs.append(fn(i))
         torch.cuda.synchronize()
-        for rep in range(3):  # replays interleaved with eager work must match eager results
-            graph.replay()
-            torch.cuda.synchronize()
-            for i in range(POOLS):
-                if not torch.equal(outs[i], eager[i]):
-                    print(json.dumps({"error": f"graph replay {rep} differs from eager for pool {i}"}), flush=True)
-                    sys.exit(1)
-            layer(rep).clone()
-            torch.cuda.synchronize()
-        reps = max(1, args.steps // POOLS)
-        us_per_layer = time_steps(lambda i: graph.replay(), reps, max(1, args.warmup // POOLS)) / POOLS
-        steps_timed = reps * POOLS
-    else:
-        us_per_layer = time_steps(layer, args.steps, args.warmup)
-        steps_timed = args.steps
-    eager_us = time_steps(layer, max(POOLS, args.steps // 2), args.warmup)
+        return graph, outs
 
-    # per-kernel averages (graph of back-to-back launches of one kernel kind, rotating pools)
+    # the timed steps: K eager layers, each one attention_matrix call, rotating over the pools
+    us_per_layer = time_steps(layer, args.steps, args.warmup)
+    steps_timed = args.steps
+
+    # the same layers replayed from a HIP graph (a checking graph first keeps a copy of every output)
+    check, outs = capture(lambda i: layer(i).clone(), POOLS)
+    for rep in range(3):  # replays interleaved with eager work must match eager results
+        check.replay()
+        torch.cuda.synchronize()
+        for i in range(POOLS):
+            if not torch.equal(outs[i], eager[i]):
+                print(json.dumps({"error": f"graph replay {rep} differs from eager for pool {i}"}), flush=True)
+                sys.exit(1)
+        layer(rep).clone()
+        torch.cuda.synchronize()
+    del check, outs
+    graph, _ = capture(layer, POOLS)
+    graph.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(prepared.out, eager[POOLS - 1]):
+        print(json.dumps({"error": "timed graph's last layer differs from eager"}), flush=True)
+        sys.exit(1)
+    graph_us = time_steps(lambda i: graph.replay(), max(1, args.steps // POOLS), max(1, args.warmup // POOLS)) / POOLS
+
+    # per-kernel averages over launches of one kernel kind, rotating pools
     kernel_us = {}
     kind_names = {_native.TA_SMALL: "segment_small", _native.TA_LARGE64: "segment_large64",
                   _native.TA_LARGE128: "segment_large128", _native.TA_LARGE256: "segment_large256"}
@@ -158,18 +179,16 @@ def main():
             continue
         launches[name] = lambda i, kind=kind: segment(qd, pools[i % POOLS][0], pools[i % POOLS][1], prepared, kind)
     launches["merge"] = lambda i: merge(prepared)
+    kernel_slot_us = {}
     for name, fn in launches.items():
-        kg = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(stream)
-        with torch.cuda.stream(side):
-            fn(0)
-        stream.wait_stream(side)
-        with torch.cuda.graph(kg, stream=side):
-            for i in range(POOLS):
-                fn(i)
-        kernel_us[name] = time_steps(lambda i: kg.replay(), max(1, args.steps // POOLS),
-                                     max(1, args.warmup // POOLS)) / POOLS
+        # the kernel's own duration: dispatch begin/end stamps of every launch (hipExtLaunchKernel events)
+        for i in range(args.warmup):
+            fn(i)
+        kernel_us[name] = statistics.mean(launch_durations_us(fn, max(POOLS, args.steps)))
+        # its slot in a graph of back-to-back launches, inter-launch gaps included
+        kg, _ = capture(fn, POOLS)
+        kernel_slot_us[name] = time_steps(lambda i: kg.replay(), max(1, args.steps // POOLS),
+                                          max(1, args.warmup // POOLS)) / POOLS
 
     # per-request execution through the same kernels (the "faster than per-request" check)
     req_prepared = prepare(schedule(tree, HQ, HK, D, "request", model), qd)
@@ -178,11 +197,10 @@ def main():
 
     # ---- roofline of the dominant kernel
     jobs = prepared.jobs
-    small_tokens = sum(len(j.tokens) for j in jobs if len(j.requests) * (HQ // HK) <= 16)
-    large_tokens = sum(len(j.tokens) for j in jobs if len(j.requests) * (HQ // HK) > 16)
+    small_rows = HQ // HK
+    small_tokens = sum(len(j.tokens) for j in jobs if len(j.requests) * small_rows <= 16)
     large_flops = sum(4 * len(j.requests) * HQ * len(j.tokens) * D for j in jobs
-                      if len(j.requests) * (HQ // HK) > 16)
-    seg_kernels = {n: t for n, t in kernel_us.items() if n.startswith("segment")}
+                      if len(j.requests) * small_rows > 16)
     dominant = max(kernel_us, key=kernel_us.get)
     traffic = _pmc_traffic(dominant)
     if dominant.startswith("segment_large"):
@@ -190,7 +208,7 @@ def main():
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1),
                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
-                    "algorithmic": f"{large_flops} FLOP per launch (4*rows*tokens*D over large jobs)"}
+                    "algorithmic": f"{large_flops} FLOP per launch (4 x rows x tokens x D over the large jobs)"}
     else:
         nbytes = physical_kv_bytes(small_tokens) if dominant == "segment_small" else \
             2 * sum(len(j.requests) for j in jobs) * HQ * (D + 1) * 4
@@ -201,7 +219,6 @@ def main():
 
     kv_bytes = physical_kv_bytes(T)
     value = kv_bytes / (us_per_layer * 1e-6) / 1e9
-    cpu = cpu_baseline(q, k, v, tree, plan, args.cpu_budget_s)
     line = {
         "metric": "tree-attn decode µs/layer at 128×8192 (8128 shared); physical-KV HBM GB/s",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps_timed, "warmup": args.warmup,
@@ -212,15 +229,16 @@ def main():
                                "(16,320 physical / 1,048,576 logical KV positions), 32Q/8KV heads, d=128, "
                                "one decode-step attention layer",
                    "method": args.method, "cost_model": args.cost_model, "kv_pools": POOLS,
-                   "timing": "hip-graph replay" if use_graph else "eager", "physical_kv_bytes": kv_bytes},
+                   "timing": "eager", "physical_kv_bytes": kv_bytes},
         "layer_hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "eager_us_per_layer": round(eager_us, 3),
+        "graph_us_per_layer": round(graph_us, 3),
         "per_request_us_per_layer": round(per_request_us, 3),
-        "speedup_vs_per_request": round(per_request_us / eager_us, 3),
+        "speedup_vs_per_request": round(per_request_us / us_per_layer, 3),
         "kernel_us": {n: round(t, 3) for n, t in kernel_us.items()},
+        "kernel_graph_slot_us": {n: round(t, 3) for n, t in kernel_slot_us.items()},
         "plan": {"jobs": len(jobs), "small_jobs": prepared.small_jobs, "plan_us": round(plan_us, 1),
                  "metadata_us": round(metadata_us, 1), "estimated_us": plan.estimated_us,
-                 "small_tokens": small_tokens, "large_tokens": large_tokens},
+                 "small_tokens": small_tokens, "large_flops": large_flops},
         "rel_l2_vs_fp32": rel,
         "roofline": roofline,
         "cpu_baseline": cpu,
@@ -229,7 +247,7 @@ def main():
 
 
 def _pmc_traffic(kernel_name):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if one exists."""
+    """HBM bytes per launch of ``kernel_name`` from the committed rocprofv3 PMC summary, if any."""
     path = ROOT / "profiles" / "pmc_traffic.json"
     if not path.exists():
         return None
@@ -240,10 +258,16 @@ def _pmc_traffic(kernel_name):
         return None
 
 
-def cpu_baseline(q, k, v, tree, plan, budget_s):
-    """Oracle (FP32 torch-CPU restatement of reference.py) on the same layer, host cores."""
+def cpu_baseline(q, k, v, tree, plan, gpu_out, budget_s):
+    """CPU leg: the FP32 oracle on the host cores (timed), and the parity check of ``gpu_out``.
+
+    Times the oracle's plan-driven ``segmented_attention`` (reference.py:16-33)
+    on the same layer and plan (median of up to 5 runs within ``budget_s``),
+    and returns the relative L2 of the GPU output against the oracle's
+    ``request_attention`` (reference.py:4-13).
+    """
     import torch
-    from oracle.attention_oracle import segmented_attention
+    from oracle.attention_oracle import relative_l2, request_attention, segmented_attention
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     qf, kf, vf = q.float(), k.float(), v.float()
@@ -257,11 +281,13 @@ def cpu_baseline(q, k, v, tree, plan, budget_s):
             break
     us = statistics.median(times) * 1e6
     gbs = physical_kv_bytes(tree.storage_tokens) / (us * 1e-6) / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "us_per_layer": round(us, 1), "cores": cores,
-            "threads": torch.get_num_threads(), "kind": "port",
-            "sample": f"{len(times)} full layer(s) of the same workload and plan through the oracle's "
-                      f"segmented_attention in fp32 (median)",
-            "cpu": platform.processor() or platform.machine()}
+    rel = relative_l2(gpu_out, request_attention(qf, kf, vf, tree))
+    cpu = {"value": round(gbs, 3), "unit": "GB/s", "us_per_layer": round(us, 1), "cores": cores,
+           "threads": torch.get_num_threads(), "kind": "port",
+           "sample": f"{len(times)} full layer(s) of the same workload and plan through the oracle's "
+                     f"segmented_attention in fp32 (median)",
+           "cpu": platform.processor() or platform.machine()}
+    return cpu, rel
 
 
 if __name__ == "__main__":

@@ -96,6 +96,15 @@ int ta_merge(const float *part, const float *lse, const int32_t *slots,
 int ta_attention_matrix(const void *q, const void *kp, const void *vp,
                         int32_t tcap, const ta_plan *plan, void *out, void *stream);
 
+/* Kernel timing hook.  No counterpart in the reference, which times kernels
+ * with device events around whole launches (scripts/profile_kernel.py:17-33).
+ * The next kernel this library launches on the calling host thread records
+ * `start_event` when its dispatch begins and `stop_event` when it ends
+ * (hipExtLaunchKernel); the hook then clears itself.  Both are hipEvent_t
+ * created with timing enabled, or both NULL to clear the hook.  Not for use
+ * under stream capture. */
+int ta_time_next_launch(void *start_event, void *stop_event);
+
 #ifdef __cplusplus
 }
 #endif

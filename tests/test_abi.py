@@ -38,6 +38,9 @@ def test_library_rejects_bad_arguments_without_gpu_work():
     assert lib.ta_segment(None, None, None, None, None, None, None, None, None, 1, 0, None, None,
                           1, 30, 8, 128, 16, 1, 0, None) == 1001
     assert lib.ta_attention_matrix(None, None, None, 1, None, None, None) == 1001
+    # the timing hook takes both events or neither; NULL/NULL clears it
+    assert lib.ta_time_next_launch(None, None) == 0
+    assert lib.ta_time_next_launch(ctypes.c_void_p(16), None) == 1001
 
 
 def test_plan_struct_layout_matches_header(tmp_path):

@@ -356,16 +356,16 @@ template <int D, bool FP16>
 hipError_t launch_d(const SegParams &sp, int kind, hipStream_t stream) {
     switch (kind) {
         case TA_SMALL:  // one wave per (job, head); one stage so that four fit on a CU
-            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 1, 1, 1>), dim3(sp.n_items), dim3(64), 0, stream, sp);
+            TA_LAUNCH((seg_tile_kernel<D, FP16, 1, 1, 1>), dim3(sp.n_items), dim3(64), stream, sp);
             break;
         case TA_LARGE64:
-            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 1, 4, 3>), dim3(sp.n_items), dim3(256), 0, stream, sp);
+            TA_LAUNCH((seg_tile_kernel<D, FP16, 1, 4, 3>), dim3(sp.n_items), dim3(256), stream, sp);
             break;
         case TA_LARGE128:
-            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 2, 4, 3>), dim3(sp.n_items), dim3(256), 0, stream, sp);
+            TA_LAUNCH((seg_tile_kernel<D, FP16, 2, 4, 3>), dim3(sp.n_items), dim3(256), stream, sp);
             break;
         case TA_LARGE256:
-            hipLaunchKernelGGL((seg_tile_kernel<D, FP16, 2, 8, 3>), dim3(sp.n_items), dim3(512), 0, stream, sp);
+            TA_LAUNCH((seg_tile_kernel<D, FP16, 2, 8, 3>), dim3(sp.n_items), dim3(512), stream, sp);
             break;
         default:
             return hipErrorNotSupported;

@@ -2,6 +2,7 @@
 // segment kernels of libtree_attn.so (internal; not part of the C ABI).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -86,6 +87,26 @@ struct SegParams {
     int n_items, hq, hk, group, tcap, maxr;
     float scale_log2;  // log2(e) / sqrt(D)
 };
+
+// Kernel timing hook (ta_time_next_launch): when set, the next kernel this
+// library launches on the calling host thread goes through hipExtLaunchKernel,
+// which stamps `start` when the dispatch begins and `stop` when it ends; the
+// hook then clears itself.
+struct LaunchEvents {
+    hipEvent_t start, stop;
+};
+extern thread_local LaunchEvents g_launch_events;
+
+#define TA_LAUNCH(KERNEL, GRID, BLOCK, STREAM, ...)                                                   \
+    do {                                                                                              \
+        const ta::LaunchEvents ev_ = ta::g_launch_events;                                             \
+        if (ev_.start) {                                                                              \
+            ta::g_launch_events = ta::LaunchEvents{nullptr, nullptr};                                 \
+            hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, 0, STREAM, ev_.start, ev_.stop, 0, __VA_ARGS__); \
+        } else {                                                                                      \
+            hipLaunchKernelGGL(KERNEL, GRID, BLOCK, 0, STREAM, __VA_ARGS__);                          \
+        }                                                                                             \
+    } while (0)
 
 // Large-job launcher of segment_tile.hip (gfx950 LDS-transpose kernels).
 // Returns hipErrorNotSupported when the shape is outside what it handles.

@@ -510,17 +510,17 @@ hipError_t launch_segment(const SegParams &sp, int kind, hipStream_t stream) {
     switch (kind) {
         case TA_SMALL: {
             const int blocks = sp.n_items < SMALL_MAX_BLOCKS ? sp.n_items : SMALL_MAX_BLOCKS;
-            hipLaunchKernelGGL((seg_small_kernel<D, FP16>), dim3(blocks), dim3(SMALL_NT), 0, stream, sp);
+            TA_LAUNCH((seg_small_kernel<D, FP16>), dim3(blocks), dim3(SMALL_NT), stream, sp);
             break;
         }
         case TA_LARGE64:
-            hipLaunchKernelGGL((seg_large_kernel<D, FP16, 1, 4, 64>), dim3(sp.n_items), dim3(256), 0, stream, sp);
+            TA_LAUNCH((seg_large_kernel<D, FP16, 1, 4, 64>), dim3(sp.n_items), dim3(256), stream, sp);
             break;
         case TA_LARGE128:
-            hipLaunchKernelGGL((seg_large_kernel<D, FP16, 2, 4, 64>), dim3(sp.n_items), dim3(256), 0, stream, sp);
+            TA_LAUNCH((seg_large_kernel<D, FP16, 2, 4, 64>), dim3(sp.n_items), dim3(256), stream, sp);
             break;
         case TA_LARGE256:
-            hipLaunchKernelGGL((seg_large_kernel<D, FP16, 2, 8, 128>), dim3(sp.n_items), dim3(512), 0, stream, sp);
+            TA_LAUNCH((seg_large_kernel<D, FP16, 2, 8, 128>), dim3(sp.n_items), dim3(512), stream, sp);
             break;
         default:
             return (hipError_t)TA_ERR_ARG;
@@ -532,7 +532,7 @@ template <int D, bool FP16>
 hipError_t launch_merge(const float *part, const float *lse, const int32_t *slots, const int32_t *counts,
                         void *out, int nreq, int hq, int maxs, hipStream_t stream) {
     constexpr int MH = NT / (D / 4);
-    hipLaunchKernelGGL((merge_kernel<D, FP16>), dim3(nreq, (hq + MH - 1) / MH), dim3(NT), 0, stream, part,
+    TA_LAUNCH((merge_kernel<D, FP16>), dim3(nreq, (hq + MH - 1) / MH), dim3(NT), stream, part,
                        lse, slots, counts, static_cast<u16 *>(out), hq, maxs);
     return hipGetLastError();
 }
@@ -552,6 +552,10 @@ int check_common(int hq, int hk, int d, int dtype) {
                  : ((fp16) ? CALL(32, true) : CALL(32, false)))
 
 }  // namespace
+
+namespace ta {
+thread_local LaunchEvents g_launch_events = {nullptr, nullptr};
+}  // namespace ta
 
 extern "C" {
 
@@ -613,6 +617,12 @@ int ta_merge(const float *part, const float *lse, const int32_t *slots, const in
 #define TA_MRG(D, F) launch_merge<D, F>(part, lse, slots, counts, out, nreq, hq, maxs, st)
     return (int)TA_DISPATCH(d, dtype == TA_FP16, TA_MRG);
 #undef TA_MRG
+}
+
+int ta_time_next_launch(void *start_event, void *stop_event) {
+    if ((start_event == nullptr) != (stop_event == nullptr)) return TA_ERR_ARG;
+    ta::g_launch_events = ta::LaunchEvents{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
+    return 0;
 }
 
 int ta_attention_matrix(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan,

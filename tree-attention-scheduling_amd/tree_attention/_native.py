@@ -22,7 +22,8 @@ KIND_ROWS = {TA_LARGE64: 64, TA_LARGE128: 128, TA_LARGE256: 256}
 _c_i32 = ctypes.c_int32
 _c_ptr = ctypes.c_void_p
 
-EXPORTS = ("ta_version", "ta_error_string", "ta_segment", "ta_merge", "ta_attention_matrix")
+EXPORTS = ("ta_version", "ta_error_string", "ta_segment", "ta_merge", "ta_attention_matrix",
+           "ta_time_next_launch")
 
 
 class TaPlan(ctypes.Structure):
@@ -70,6 +71,8 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         lib.ta_attention_matrix.restype = ctypes.c_int
         lib.ta_attention_matrix.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_i32, ctypes.POINTER(TaPlan),
                                             _c_ptr, _c_ptr]
+        lib.ta_time_next_launch.restype = ctypes.c_int
+        lib.ta_time_next_launch.argtypes = [_c_ptr, _c_ptr]
         if path is None:
             _lib = lib
         return lib

@@ -314,6 +314,32 @@ def merge(prepared):
     return p.out
 
 
+def launch_durations_us(fn, n: int, device=None) -> list:
+    """Kernel durations of ``n`` eager calls ``fn(0..n-1)`` on the current stream, in microseconds.
+
+    Each call's first kernel launch of this library is stamped at dispatch
+    begin and end through ``ta_time_next_launch`` (hipExtLaunchKernel), so the
+    figures are the kernel's own duration, without launch gaps -- the same
+    quantity ``rocprofv3 --kernel-trace`` reports.  Not for use under capture.
+    """
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    stream = torch.cuda.current_stream(device)
+    lib = _native.load()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for start, stop in events:  # a first record creates the underlying HIP events
+        start.record(stream)
+        stop.record(stream)
+    torch.cuda.synchronize(device)
+    try:
+        for i, (start, stop) in enumerate(events):
+            _native.check(lib.ta_time_next_launch(start.cuda_event, stop.cuda_event))
+            fn(i)
+    finally:
+        lib.ta_time_next_launch(None, None)
+    torch.cuda.synchronize(device)
+    return [start.elapsed_time(stop) * 1e3 for start, stop in events]
+
+
 class CachedDecodePlan:
     """A prompt schedule plus one contiguous growing KV tail per request (kernels.py:171-186)."""
 
