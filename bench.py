@@ -6,7 +6,8 @@ Workload: 128 requests, one 8128-token shared root plus 64 private tokens each
 (16,320 physical vs 1,048,576 logical KV positions), 32 query / 8 KV heads,
 head dim 128, bf16, Q/K/V ~ N(0, 1) from a fixed seed, subset-DP (``cube``)
 plan under the MI355X cost model.  One step = one ``attention_matrix`` call
-(segment kernels + merge) on resident pools.  Steps rotate over 8 distinct KV
+(the root's segment kernel, then the tail kernel whose work items also merge
+each request) on resident pools.  Steps rotate over 8 distinct KV
 pools (535 MB, above the 256 MB MALL) so the bandwidth is HBM bandwidth.
 
 Timing: HIP events on the launch stream around exactly K eager steps after W
@@ -75,7 +76,8 @@ def main():
     import torch
     from tree_attention import CostModel, schedule, shapes
     from tree_attention import _native
-    from tree_attention.kernels import attention_matrix, launch_durations_us, merge, pack_kv, prepare, segment
+    from tree_attention.kernels import (attention_matrix, launch_durations_us, merge, pack_kv, prepare, segment,
+                                        tail_merge)
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -178,7 +180,11 @@ def main():
         if prepared.abi.n_items[kind] == 0:
             continue
         launches[name] = lambda i, kind=kind: segment(qd, pools[i % POOLS][0], pools[i % POOLS][1], prepared, kind)
-    launches["merge"] = lambda i: merge(prepared)
+    if prepared.abi.n_items[_native.TA_TAIL]:
+        # the fused kind: each tail item attends its request's tail and merges the request
+        launches["segment_tail_merge"] = lambda i: tail_merge(qd, pools[i % POOLS][0], pools[i % POOLS][1], prepared)
+    if prepared.abi.n_rest:
+        launches["merge"] = lambda i: merge(prepared)  # all requests; the layer merges only `rest`
     kernel_slot_us = {}
     for name, fn in launches.items():
         # the kernel's own duration: dispatch begin/end stamps of every launch (hipExtLaunchKernel events)
@@ -199,6 +205,9 @@ def main():
     jobs = prepared.jobs
     small_rows = HQ // HK
     small_tokens = sum(len(j.tokens) for j in jobs if len(j.requests) * small_rows <= 16)
+    tail_jobs = sorted({j for j, _, _ in prepared.items[_native.TA_TAIL].view(-1, 3).tolist()})
+    tail_requests = [jobs[j].requests[0] for j in tail_jobs]
+    counts = prepared.counts.tolist()
     large_flops = sum(4 * len(j.requests) * HQ * len(j.tokens) * D for j in jobs
                       if len(j.requests) * small_rows > 16)
     dominant = max(kernel_us, key=kernel_us.get)
@@ -210,8 +219,15 @@ def main():
                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                     "algorithmic": f"{large_flops} FLOP per launch (4 x rows x tokens x D over the large jobs)"}
     else:
-        nbytes = physical_kv_bytes(small_tokens) if dominant == "segment_small" else \
-            2 * sum(len(j.requests) for j in jobs) * HQ * (D + 1) * 4
+        if dominant == "segment_small":
+            nbytes = physical_kv_bytes(small_tokens)
+        elif dominant == "segment_tail_merge":
+            # tail KV, the other partial slots of each tail request (o and lse), the output rows
+            nbytes = (physical_kv_bytes(sum(len(jobs[j].tokens) for j in tail_jobs))
+                      + sum(counts[r] - 1 for r in tail_requests) * HQ * (D + 1) * 4
+                      + len(tail_requests) * HQ * D * 2)
+        else:
+            nbytes = sum(counts) * HQ * (D + 1) * 4 + len(counts) * HQ * D * 2
         achieved = nbytes / (kernel_us[dominant] * 1e-6) / 1e9
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -44,6 +44,13 @@ extern "C" {
 #define TA_LARGE64 1    /* row tiles of 64 rows  */
 #define TA_LARGE128 2   /* row tiles of 128 rows */
 #define TA_LARGE256 3   /* row tiles of 256 rows */
+#define TA_TAIL 4       /* single-request jobs that are their request's only job of
+                           <= 16 rows (first row 0): in ta_attention_matrix and
+                           ta_tail_merge the item also merges its request's other
+                           partial slots and writes out; through ta_segment it
+                           writes its partial like TA_SMALL.  The job's own slot
+                           is the last of its request's slots. */
+#define TA_NKINDS 5
 
 #define TA_ERR_ARG 1001      /* null pointer, bad size or unsupported shape */
 #define TA_ERR_ALIGN 1002    /* q / kp / vp / part / out not 16-byte aligned */
@@ -59,12 +66,15 @@ typedef struct ta_plan {
     const int32_t *rowbase;   /* [njobs] first partial slot of each job            */
     const int32_t *slots;     /* [nreq * maxs] partial slots of each request       */
     const int32_t *counts;    /* [nreq] number of slots of each request            */
-    const int32_t *items[4];  /* work-item triples per kind TA_SMALL .. TA_LARGE256 */
-    int32_t n_items[4];       /* number of triples per kind                        */
+    const int32_t *items[TA_NKINDS];  /* work-item triples per kind TA_SMALL .. TA_TAIL */
+    int32_t n_items[TA_NKINDS];       /* number of triples per kind                 */
+    const int32_t *rest;      /* [n_rest] requests without a TA_TAIL job: the ones
+                                 the merge kernel of ta_attention_matrix covers    */
     float *part;
     float *lse;
     int32_t njobs, maxr, maxs, nreq, nslot;
     int32_t hq, hk, d, dtype;
+    int32_t n_rest;
 } ta_plan;
 
 /* Version string of the library build. */
@@ -91,10 +101,22 @@ int ta_merge(const float *part, const float *lse, const int32_t *slots,
              const int32_t *counts, void *out, int32_t nreq, int32_t hq,
              int32_t d, int32_t maxs, int32_t dtype, void *stream);
 
-/* One decode-step attention layer on resident pools: every segment launch of
- * the plan followed by the merge (replaces attention_matrix, kernels.py:152-168). */
+/* One decode-step attention layer on resident pools (replaces attention_matrix,
+ * kernels.py:152-168): the large-job segment launches, the small-job launch,
+ * the TA_TAIL launch that merges the requests owning a tail job, and the merge
+ * of the remaining requests (`rest`).  Pools whose capacity is not a multiple
+ * of 8 take the unfused order: every segment kind, then the merge of all
+ * requests. */
 int ta_attention_matrix(const void *q, const void *kp, const void *vp,
                         int32_t tcap, const ta_plan *plan, void *out, void *stream);
+
+/* The TA_TAIL launch of ta_attention_matrix on its own: each work item attends
+ * its request's tail job and merges the request's other partial slots (written
+ * before, on the same stream) into `out`.  No counterpart in the reference: a
+ * fusion of _segment (kernels.py:8-55) for these jobs with _merge
+ * (kernels.py:58-83).  Needs tcap % 8 == 0 (TA_ERR_ARG otherwise). */
+int ta_tail_merge(const void *q, const void *kp, const void *vp,
+                  int32_t tcap, const ta_plan *plan, void *out, void *stream);
 
 /* Kernel timing hook.  No counterpart in the reference, which times kernels
  * with device events around whole launches (scripts/profile_kernel.py:17-33).

@@ -16,7 +16,8 @@ from oracle.attention_oracle import relative_l2, request_attention
 from tree_attention import CostModel, KVTree, schedule, shapes
 from tree_attention import _native
 from tree_attention.kernels import (CachedDecodePlan, attention, attention_matrix, merge, pack_kv, prepare,
-                                    segment)
+                                    segment, tail_merge)
+from tree_attention.schedule import Job, Plan
 
 pytestmark = pytest.mark.gpu
 METHODS = ("request", "fixed", "greedy", "cube")
@@ -186,21 +187,66 @@ def test_large_row_tiles_all_kinds(pad, dtype, device):
         check(out, ref, 0.008, 0.03, "large-tiles")
 
 
-def test_attention_packs_and_c_abi_phases_agree(device):
+@pytest.mark.parametrize("name", ["deep", "wide"])
+def test_attention_packs_and_c_abi_phases_agree(name, device):
     """attention(q,k,v) == attention_matrix on packed pools == explicit ta_segment + ta_merge calls."""
-    tree = shapes.tree(shapes.benchmark_cases()["deep"])
+    tree = shapes.tree(shapes.benchmark_cases()[name])
     q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 3)
     qd, kd, vd = q.to(device), k.to(device), v.to(device)
-    prepared = prepare(schedule(tree, method="cube"), qd)
+    prepared = prepare(schedule(tree, method="cube", model=MI355X_LIKE), qd)
     a = attention(qd, kd, vd, prepared).clone()
     kp, vp = pack_kv(kd, vd)
     b = attention_matrix(qd, kp, vp, prepared).clone()
+    assert (prepared.abi.n_items[_native.TA_TAIL] > 0) == (name == "wide")
     prepared.out.zero_()
-    for kind in range(4):
+    for kind in range(_native.TA_NKINDS):
         segment(qd, kp, vp, prepared, kind)
     c = merge(prepared).clone()
     torch.cuda.synchronize()
-    assert torch.equal(a, b) and torch.equal(b, c)
+    assert torch.equal(a, b)
+    if prepared.abi.n_rest == 0:
+        # the fused path on its own: partial-producing kinds, then the tail items merge
+        prepared.out.zero_()
+        for kind in (_native.TA_LARGE256, _native.TA_LARGE128, _native.TA_LARGE64, _native.TA_SMALL):
+            segment(qd, kp, vp, prepared, kind)
+        d = tail_merge(qd, kp, vp, prepared).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(b, d)
+    # the unfused order merges in another order: equal up to rounding
+    assert relative_l2(b.cpu(), c.cpu().float()) < 5e-4
+
+
+class _Paths:
+    def __init__(self, paths):
+        self.paths = paths
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_tail_items_with_merge_rest(dtype, device):
+    """Requests merged by their TA_TAIL item next to requests left to the merge kernel."""
+    jobs = [Job(tuple(range(6)), tuple(range(0, 300))),       # 24 rows: large, all requests
+            Job((0,), tuple(range(300, 364))),                 # request 0: one tail (fused merge)
+            Job((1,), tuple(range(370, 380))), Job((1,), tuple(range(450, 520))),  # two small jobs
+            Job((2, 3), tuple(range(380, 400))),               # 2 and 3 share a small job
+            Job((5,), tuple(range(400, 401))),                 # request 5: a one-token tail
+            Job((4, 5), tuple(range(401, 450)))]               # ... and a large-free shared job
+    paths = [[] for _ in range(6)]
+    for job in jobs:
+        for r in job.requests:
+            paths[r].extend(job.tokens)
+    tree = _Paths([tuple(p) for p in paths])
+    g = torch.Generator().manual_seed(17)
+    q = torch.randn(6, 16, 128, generator=g).to(dtype)
+    k = torch.randn(528, 4, 128, generator=g).to(dtype)
+    v = torch.randn(528, 4, 128, generator=g).to(dtype)
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    prepared = prepare(Plan(jobs, "x", 0.0, dict(kvheads=4)), qd)
+    tails = {prepared.jobs[j].requests for j, _, _ in prepared.items[_native.TA_TAIL].view(-1, 3).tolist()}
+    assert tails == {(0,)} and prepared.rest.tolist() == [1, 2, 3, 4, 5]
+    out = attention_matrix(qd, kp, vp, prepared)
+    torch.cuda.synchronize()
+    check(out, oracle_fp32(q, k, v, tree), 0.006, 0.02, "tail+rest")
 
 
 def test_cached_decode_plan_steps(device):

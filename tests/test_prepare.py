@@ -42,10 +42,14 @@ def test_metadata_layout_small_first_and_compact_slots():
     for r in range(128):
         assert {slot_owner[s] for s in p.slots[r, :counts[r]].tolist()} == {r}
     assert p.part.shape == (sum(qlen), 32, 128) and p.lse.shape == (sum(qlen), 32)
-    # work items: one per (small job, head); large jobs of 16 requests = 64 rows -> one 64-row tile per head
-    assert p.abi.n_items[_native.TA_SMALL] == 128 * 8
-    small = p.items[_native.TA_SMALL].view(-1, 3).tolist()
-    assert sorted(small) == [[j, 0, h] for j in range(128) for h in range(8)]
+    # work items: one per (small job, head); every private tail is its request's only
+    # small job, so all are TA_TAIL items that merge their request and no request is
+    # left for the merge kernel; large jobs of 16 requests = 64 rows -> one 64-row tile per head
+    assert p.abi.n_items[_native.TA_SMALL] == 0
+    assert p.abi.n_items[_native.TA_TAIL] == 128 * 8
+    tails = p.items[_native.TA_TAIL].view(-1, 3).tolist()
+    assert sorted(tails) == [[j, 0, h] for j in range(128) for h in range(8)]
+    assert p.abi.n_rest == 0 and p.rest.numel() == 0
     assert p.abi.n_items[_native.TA_LARGE64] == 32 * 8
     items = p.items[_native.TA_LARGE64].view(-1, 3).tolist()
     assert sorted(set((j, h) for j, _, h in items)) == [(j, h) for j in range(128, 160) for h in range(8)]
@@ -113,3 +117,25 @@ def test_cached_decode_plan_tails():
     assert all(p.klen[i].item() == len(p.jobs[i].tokens) for i in others)
     with pytest.raises(ValueError):
         cached.update(6)
+
+
+def test_tail_items_and_merge_rest():
+    """TA_TAIL: single-request small jobs that are their request's only small job."""
+    q = torch.empty(4, 8, 32, dtype=torch.float16)
+    settings = dict(kvheads=2)
+    jobs = [Job((0, 1, 2, 3), tuple(range(0, 40))),   # 16 rows: small, shared by all
+            Job((0,), tuple(range(40, 50))),          # request 0 has two small jobs
+            Job((1,), tuple(range(50, 60))),          # request 1: two small jobs as well
+            Job((2,), tuple(range(60, 70)))]          # request 3 has only the shared job
+    p = prepare(Plan(jobs, "x", 0.0, settings), q)
+    assert p.abi.n_items[_native.TA_TAIL] == 0 and p.rest.tolist() == [0, 1, 2, 3]
+    jobs = [Job((0, 1, 2, 3, 4, 5), tuple(range(0, 40))),  # 24 rows: large
+            Job((0,), tuple(range(40, 50))), Job((1,), tuple(range(50, 60))),
+            Job((2, 3), tuple(range(64, 70))), Job((1,), tuple(range(70, 74)))]
+    q = torch.empty(6, 8, 32, dtype=torch.float16)
+    p = prepare(Plan(jobs, "x", 0.0, settings), q)
+    tail_jobs = sorted({j for j, _, _ in p.items[_native.TA_TAIL].view(-1, 3).tolist()})
+    assert [p.jobs[j].requests for j in tail_jobs] == [(0,)]
+    # request 1 has two small jobs, 2 and 3 share one, 4 and 5 have only the large job
+    assert p.rest.tolist() == [1, 2, 3, 4, 5] and p.abi.n_rest == 5
+    assert p.abi.n_items[_native.TA_SMALL] == 3 * 2

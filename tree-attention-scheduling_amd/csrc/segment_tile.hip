@@ -352,10 +352,462 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
     }
 }
 
+// ------------------------------------------------------------------------
+// Pipelined large-tile kernel.  The 32-token steps of a work item form one
+// software pipeline that runs across tile boundaries; within a step the
+// matrix cores and the VALU work on different steps:
+//
+//   block(g):  QK of step g+1 (MFMA)   || exponentials of step g (VALU),
+//                                          LDS reads of V(g)
+//              PV + row sums of step g  || LDS reads of K(g+2), masking and
+//                                          row maxima of step g+1
+//
+// and the rare online-softmax rescale runs between blocks.  The order inside
+// a block is pinned with sched_group_barrier so that MFMAs and VALU
+// instructions alternate in each wave's instruction stream.  K/V tiles arrive
+// by LDS DMA into four stages: tiles t and t+1 are read while t+2 and t+3 are
+// in flight, with one barrier per tile.
+template <int D, bool FP16, int NW>
+struct PipeMath {
+    static constexpr int NB = 2;
+    static constexpr int DB = D / 16;
+    static constexpr int KS = D / 32;
+    using O = Ops<FP16>;
+    using T = Tile<D>;
+    using TM = TileMath<D, FP16, NB, NW>;
+
+    f32x4 o[NB][DB], z[NB];
+    float m[NB], lm[NB];
+    f32x4 s[NB][2];      // scores of the step whose exponentials come next
+    u32x4 kf[2][KS];     // K fragments of the next QK step
+    u32x4 vf[DB];        // V^T fragments of the current PV step
+
+    __device__ void reset() {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            m[nb] = NEG_INF;
+            z[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int db = 0; db < DB; ++db) o[nb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    __device__ static void load_v(const u16 *__restrict__ st, int voff, int base, u32x4 (&v)[DB]) {
+        const u16 *vrow = st + voff + T::BLK * (T::KBLK + base / T::VROWS);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const u16 *va = vrow + 8 * T::SV * db;
+            v[db] = tr_pair(va, va + T::BLK * (16 / T::VROWS));
+        }
+    }
+
+    // Scores of a step: mask tokens outside [lo, hi) (if MASK) and take the
+    // lane-local row maxima.
+    template <bool MASK>
+    __device__ void finish_scores(f32x4 (&sn)[NB][2], int lo, int hi, int g4) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            if (MASK) {
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int tok = 16 * b + 4 * g4 + i;
+                        if (tok < lo || tok >= hi) sn[nb][b][i] = NEG_INF;
+                    }
+            }
+            lm[nb] = fmaxf(fmaxf(fmaxf(sn[nb][0][0], sn[nb][0][1]), fmaxf(sn[nb][0][2], sn[nb][0][3])),
+                           fmaxf(fmaxf(sn[nb][1][0], sn[nb][1][1]), fmaxf(sn[nb][1][2], sn[nb][1][3])));
+            s[nb][0] = sn[nb][0];
+            s[nb][1] = sn[nb][1];
+        }
+    }
+
+    // Raise the running maxima where a score of the staged step exceeds them
+    // by more than TAU (wave-uniform branch, rare after the first step).
+    __device__ void rescale(float c) {
+        bool need = false;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) need |= lm[nb] * c > m[nb] + TAU;
+        if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const float mn = fmaxf(m[nb], xor_max(lm[nb]) * c);
+                const float alpha = mn == NEG_INF ? 1.f : fast_exp2(m[nb] - mn);
+                z[nb] *= alpha;
+#pragma unroll
+                for (int db = 0; db < DB; ++db) o[nb][db] *= alpha;
+                m[nb] = mn;
+            }
+        }
+    }
+
+    // One pipeline block (see above).  vs / vbase: stage and offset of V(g);
+    // ks / kbase: of K(g+2) (any resident step when there is none); lo / hi:
+    // valid tokens of step g+1.  Every fragment register set is reloaded only
+    // after its last reader: V(g) during QK(g+1), K(g+2) during PV(g).
+    template <bool MORE, bool MASKN>
+    __device__ __forceinline__ void block(const u16 *__restrict__ vs, int vbase, const u16 *__restrict__ ks,
+                                          int kbase, const u32x4 (&qf)[NB][KS], int koff, int voff, int lo,
+                                          int hi, int g4, float c) {
+        const u32x4 ones = {O::ONE2, O::ONE2, O::ONE2, O::ONE2};
+        f32x4 sn[NB][2];
+        if (MORE) TM::qk(kf, qf, sn);
+        load_v(vs, voff, vbase, vf);
+        u32x4 pb[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            float pr[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(__builtin_fmaf(s[nb][i >> 2][i & 3], c, -m[nb]));
+            pb[nb] = u32x4{O::pack(pr[0], pr[1]), O::pack(pr[2], pr[3]), O::pack(pr[4], pr[5]),
+                           O::pack(pr[6], pr[7])};
+        }
+        if (MORE) {
+            // 2*KS*NB QK MFMAs; the V reads go out with the first half of them
+#pragma unroll
+            for (int i = 0; i < 2 * KS * NB; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                if (i < DB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+                __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);  // transcendental
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // K(g+1) is dead only after QK(g+1)
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) o[nb][db] = O::mma_k32(vf[db], pb[nb], o[nb][db]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) z[nb] = O::mma_k32(ones, pb[nb], z[nb]);
+        if (MORE) {
+            TM::load_k(ks, koff, kbase, kf);
+            finish_scores<MASKN>(sn, lo, hi, g4);
+        }
+        // instruction order: QK MFMAs alternate with the exponentials and the
+        // V reads, then PV MFMAs alternate with the K reads and the score epilogue
+        if (MORE) {
+            // DB*NB PV MFMAs; the K reads go out with the first half of them
+#pragma unroll
+            for (int i = 0; i < DB * NB; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+                if (i < 2 * KS) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);  // VALU
+            }
+        }
+    }
+};
+
+template <int D, bool FP16, int NW>
+__global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
+    using T = Tile<D>;
+    using M = PipeMath<D, FP16, NW>;
+    using TM = TileMath<D, FP16, 2, NW>;
+    constexpr int NB = M::NB, KS = M::KS;
+    constexpr int STAGES = 4;
+    constexpr int BPW = T::NBLK / NW;  // copies per wave per tile
+    static_assert(T::NBLK % NW == 0, "every wave copies the same number of blocks");
+    static_assert(2 * BPW <= 63, "two tiles of copies fit the vmcnt counter");
+    __shared__ __attribute__((aligned(16))) u16 lds[STAGES * T::ELEMS];
+
+    const int total = gridDim.x;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int q8 = total >> 3, rm = total & 7;
+    const int item = xcd * q8 + min(xcd, rm) + slot;
+    const int job = p.items[3 * item], row0 = p.items[3 * item + 1], h = p.items[3 * item + 2];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row = lane & 15, g4 = lane >> 4;
+    const int kst = p.kstart[job];
+    const int ntok = max(0, min(p.klen[job], p.tcap - kst));
+    const int kend = kst + ntok;
+    const int nrows = p.qlen[job] * p.group;
+    const int wrow0 = row0 + 16 * NB * wave;
+    const bool active = wrow0 < nrows;
+    const float c = p.scale_log2;
+
+    u32x4 qf[NB][KS];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int rr = wrow0 + 16 * nb + row;
+        if (rr < nrows) {
+            const int lr = rr / p.group, gg = rr - lr * p.group;
+            const int rq = p.qids[(size_t)job * p.maxr + lr];
+            const u16 *src = p.q + ((size_t)rq * p.hq + h * p.group + gg) * D + 8 * g4;
+#pragma unroll
+            for (int k = 0; k < KS; ++k) qf[nb][k] = *(const u32x4 *)(src + 32 * k);
+        } else {
+#pragma unroll
+            for (int k = 0; k < KS; ++k) qf[nb][k] = u32x4{0, 0, 0, 0};
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int k = 0; k < KS; ++k) asm volatile("" : "+v"(qf[nb][k]));
+
+    M acc;
+    acc.reset();
+    const int lane_ofs = 8 * (4 * ((row & 3) >> 1) + (row >> 2)) + 4 * (row & 1);
+    const int koff = T::BLK * g4 + lane_ofs;
+    const int voff = T::BLK * ((4 * g4) / T::VROWS) + 64 * (((4 * g4) % T::VROWS) >> 2) + lane_ofs;
+
+    const int tb0 = kst & ~7;
+    const int ntiles = ntok > 0 ? (kend - tb0 + T::TT - 1) / T::TT : 0;
+    const int nsteps = ntok > 0 ? (kend - tb0 + 31) / 32 : 0;
+    auto stage = [&](int g) { return lds + ((g >> 1) & (STAGES - 1)) * T::ELEMS; };
+
+    // prologue: tiles 0-2 in flight, wait for tile 0, stage step 0's scores
+    for (int t = 0; t < 3 && t < ntiles; ++t)
+        TM::copy(lds + t * T::ELEMS, p.kp, p.vp, h, p.tcap, tb0 + t * T::TT, kst, kend, wave, lane);
+    if (ntiles >= 3)
+        __builtin_amdgcn_s_waitcnt(TA_VMCNT(2 * BPW));
+    else if (ntiles == 2)
+        __builtin_amdgcn_s_waitcnt(TA_VMCNT(BPW));
+    else
+        __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
+    __builtin_amdgcn_s_barrier();
+    if (active && nsteps > 0) {
+        f32x4 s0[NB][2];
+        TM::load_k(lds, koff, 0, acc.kf);
+        TM::qk(acc.kf, qf, s0);
+        acc.template finish_scores<true>(s0, kst - tb0, kend - tb0, g4);
+        acc.rescale(c);
+        if (nsteps > 1) TM::load_k(lds, koff, 32, acc.kf);
+    }
+
+    // Entering tile t (at step 2t): tile t+1 must have landed, since this
+    // tile's first block reads its K; once every wave passed the barrier the
+    // stage of tile t-1 is free for tile t+3.
+    auto sync_tile = [&](int t) {
+        if (t + 1 >= ntiles) return;
+        if (t + 2 < ntiles)
+            __builtin_amdgcn_s_waitcnt(TA_VMCNT(BPW));
+        else
+            __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
+        __builtin_amdgcn_s_barrier();
+        if (t + 3 < ntiles)
+            TM::copy(lds + ((t + 3) & (STAGES - 1)) * T::ELEMS, p.kp, p.vp, h, p.tcap, tb0 + (t + 3) * T::TT, kst,
+                     kend, wave, lane);
+    };
+    // steady state: steps whose successor is neither the last nor masked
+    int g = 0;
+    for (; g + 2 < nsteps; ++g) {
+        if (!(g & 1)) sync_tile(g >> 1);
+        if (active) {
+            const int gk = g + 2;
+            acc.template block<true, false>(stage(g), 32 * (g & 1), stage(gk), 32 * (gk & 1), qf, koff, voff, 0, 32,
+                                            g4, c);
+            acc.rescale(c);
+        }
+    }
+    // the last two steps: the successor of step nsteps-2 may be masked at its end
+    if (g + 1 < nsteps) {
+        if (!(g & 1)) sync_tile(g >> 1);
+        if (active) {
+            const int hi = kend - (tb0 + 32 * (g + 1));
+            if (hi < 32)
+                acc.template block<true, true>(stage(g), 32 * (g & 1), stage(g + 1), 32 * ((g + 1) & 1), qf, koff,
+                                               voff, 0, hi, g4, c);
+            else
+                acc.template block<true, false>(stage(g), 32 * (g & 1), stage(g + 1), 32 * ((g + 1) & 1), qf, koff,
+                                                voff, 0, 32, g4, c);
+            acc.rescale(c);
+        }
+        ++g;
+    }
+    if (g < nsteps) {
+        if (!(g & 1)) sync_tile(g >> 1);
+        if (active) acc.template block<false, false>(stage(g), 32 * (g & 1), stage(g), 0, qf, koff, voff, 0, 32, g4, c);
+    }
+
+    if (!active) return;
+    const int rb = p.rowbase[job];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int grow = wrow0 + 16 * nb + row;
+        if (grow >= nrows) continue;
+        const int lr = grow / p.group, gg = grow - lr * p.group;
+        const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
+        float *dst = p.part + prow * D + 4 * g4;
+        const bool any = acc.m[nb] != NEG_INF;
+        const float zr = acc.z[nb][0];
+        const float inv = any ? 1.f / zr : 0.f;
+#pragma unroll
+        for (int db = 0; db < M::DB; ++db) *(f32x4 *)(dst + 16 * db) = acc.o[nb][db] * inv;
+        if (g4 == 0) p.lse[prow] = any ? (acc.m[nb] + __builtin_amdgcn_logf(zr)) * LN2 : NEG_INF;
+    }
+}
+
+// ------------------------------------------------------------------------
+// Tail kernel with the merge fused in (TA_TAIL items with out given).  One
+// wave per (tail job, KV head): the job's single request has G = hq/hk query
+// rows for this head, and every other partial slot of the request was written
+// by an earlier launch on the stream.  The wave
+//   1. starts the DMA of the tail's first K/V tile, the loads of the first
+//      PF / UPL other slots (o and lse; the job's own slot is the request's
+//      last) and the Q loads, so that the three latencies overlap;
+//   2. attends the tail (the small-job tile loop);
+//   3. puts its own normalised partial and log-sum-exp in LDS, re-read in the
+//      merge layout: lane l owns units u = l + 64k (k < UPL) of G*D/4 float4
+//      units, unit u = (row u / (D/4), d = 4 (u % (D/4)));
+//   4. merges the own partial with the other slots by the online log-sum-exp
+//      of the merge kernel and writes the output rows.
+template <int D, bool FP16, int UPL>
+__global__ __launch_bounds__(64) void seg_tail_kernel(SegParams p) {
+    using T = Tile<D>;
+    using M = TileMath<D, FP16, 1, 1>;
+    constexpr int KS = M::KS, DB = M::DB;
+    constexpr int PF = 32;          // float4 registers of prefetched slots
+    constexpr int CH = PF / UPL;    // slots per merge round
+    constexpr int DU = D / 4;       // units per row
+    constexpr float LOG2E = 1.44269504088896341f;
+    __shared__ __attribute__((aligned(16))) u16 lds[T::ELEMS];
+
+    const int item = blockIdx.x;
+    const int job = p.items[3 * item], h = p.items[3 * item + 2];
+    const int lane = threadIdx.x;
+    const int row = lane & 15, g4 = lane >> 4;
+    const int kst = p.kstart[job];
+    const int ntok = max(0, min(p.klen[job], p.tcap - kst));
+    const int kend = kst + ntok;
+    const int G = p.group;  // rows of the job (one request)
+    const int tb0 = kst & ~7;
+    const int ntiles = ntok > 0 ? (kend - tb0 + T::TT - 1) / T::TT : 0;
+    const int r = p.qids[(size_t)job * p.maxr];
+    const int own = p.rowbase[job];
+    const int cnt = p.counts[r] - 1;  // other slots; the job's own slot is the last one
+    const int32_t *slr = p.slots + (size_t)r * p.maxs;
+    const int units = G * DU;
+
+    // 1. first tile, first merge round, Q
+    if (ntiles > 0) M::copy(lds, p.kp, p.vp, h, p.tcap, tb0, kst, kend, 0, lane);
+    float l[CH][UPL];
+    f32x4 v[CH][UPL];
+    auto load_round = [&](int s0) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int si = s0 + c;
+            const int sl = slr[min(si, max(cnt - 1, 0))];
+            const bool use = si < cnt && sl != own;
+#pragma unroll
+            for (int k = 0; k < UPL; ++k) {
+                const int u = min(lane + 64 * k, units - 1);
+                const int head = h * G + u / DU;
+                const size_t prow = (size_t)sl * p.hq + head;
+                const f32x4 x = *(const f32x4 *)(p.part + prow * D + 4 * (u % DU));
+                const float lx = p.lse[prow];
+                // the own slot's row is not written on this path: keep it out
+                l[c][k] = use ? lx * LOG2E : NEG_INF;
+                v[c][k] = use ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    };
+    load_round(0);
+    u32x4 qf[1][KS];
+    {
+        const int rr = row < G ? row : 0;  // rows past G duplicate row 0; never stored
+        const u16 *src = p.q + ((size_t)r * p.hq + h * G + rr) * D + 8 * g4;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) qf[0][k] = *(const u32x4 *)(src + 32 * k);
+    }
+
+    // 2. attend the tail
+    M acc;
+    acc.reset();
+    const int lane_ofs = 8 * (4 * ((row & 3) >> 1) + (row >> 2)) + 4 * (row & 1);
+    const int koff = T::BLK * g4 + lane_ofs;
+    const int voff = T::BLK * ((4 * g4) / T::VROWS) + 64 * (((4 * g4) % T::VROWS) >> 2) + lane_ofs;
+    for (int it = 0; it < ntiles; ++it) {
+        const int t0 = tb0 + it * T::TT;
+        if (it > 0) M::copy(lds, p.kp, p.vp, h, p.tcap, t0, kst, kend, 0, lane);
+        __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
+        acc.tile(lds, qf, koff, voff, max(0, kst - t0), min(T::TT, kend - t0), g4, p.scale_log2);
+    }
+
+    // 3. own partial through LDS into the merge layout (the tile stage is free:
+    //    its reads fed the MFMAs above)
+    float *opart = reinterpret_cast<float *>(lds);  // [G][D] normalised partial
+    float *olse = opart + 16 * D;                   // [G] log-sum-exp, log2 units
+    {
+        const bool any = acc.m[0] != NEG_INF;
+        const float zr = acc.z[0][0];
+        const float inv = any ? 1.f / zr : 0.f;
+        if (row < G) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+                *(f32x4 *)(opart + row * D + 16 * db + 4 * g4) = acc.o[0][db] * inv;
+            if (g4 == 0) olse[row] = any ? acc.m[0] + __builtin_amdgcn_logf(zr) : NEG_INF;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
+    float Mx[UPL], Z[UPL];
+    f32x4 o[UPL];
+#pragma unroll
+    for (int k = 0; k < UPL; ++k) {
+        const int u = min(lane + 64 * k, units - 1);
+        Mx[k] = olse[u / DU];
+        Z[k] = Mx[k] == NEG_INF ? 0.f : 1.f;
+        o[k] = *(const f32x4 *)(opart + (u / DU) * D + 4 * (u % DU));
+    }
+
+    // 4. merge the other slots, CH per round
+    for (int s0 = 0;;) {
+#pragma unroll
+        for (int k = 0; k < UPL; ++k) {
+            float cm = Mx[k];
+#pragma unroll
+            for (int c = 0; c < CH; ++c) cm = fmaxf(cm, l[c][k]);
+            const float alpha = Mx[k] == NEG_INF ? 0.f : fast_exp2(Mx[k] - cm);
+            Z[k] *= alpha;
+            o[k] *= alpha;
+            Mx[k] = cm;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const float w = l[c][k] == NEG_INF ? 0.f : fast_exp2(l[c][k] - cm);
+                Z[k] += w;
+                o[k] += w * v[c][k];
+            }
+        }
+        s0 += CH;
+        if (s0 >= cnt) break;
+        load_round(s0);
+    }
+#pragma unroll
+    for (int k = 0; k < UPL; ++k) {
+        const int u = lane + 64 * k;
+        if (u >= units) continue;
+        const f32x4 a = o[k] * (Z[k] > 0.f ? 1.f / Z[k] : 0.f);
+        u16 *dst = p.out + ((size_t)r * p.hq + h * G + u / DU) * D + 4 * (u % DU);
+        *(u32x2 *)dst = u32x2{Ops<FP16>::pack(a[0], a[1]), Ops<FP16>::pack(a[2], a[3])};
+    }
+}
+
+template <int D, bool FP16>
+hipError_t launch_tail_merge(const SegParams &sp, hipStream_t stream) {
+    // float4 units per lane: G*D/4 units over 64 lanes
+    const int units = sp.group * (D / 4);
+    if (units <= 64)
+        TA_LAUNCH((seg_tail_kernel<D, FP16, 1>), dim3(sp.n_items), dim3(64), stream, sp);
+    else if (units <= 128)
+        TA_LAUNCH((seg_tail_kernel<D, FP16, 2>), dim3(sp.n_items), dim3(64), stream, sp);
+    else if (units <= 256)
+        TA_LAUNCH((seg_tail_kernel<D, FP16, 4>), dim3(sp.n_items), dim3(64), stream, sp);
+    else if (units <= 512)
+        TA_LAUNCH((seg_tail_kernel<D, FP16, 8>), dim3(sp.n_items), dim3(64), stream, sp);
+    else
+        return hipErrorNotSupported;
+    return hipGetLastError();
+}
+
 template <int D, bool FP16>
 hipError_t launch_d(const SegParams &sp, int kind, hipStream_t stream) {
     switch (kind) {
         case TA_SMALL:  // one wave per (job, head); one stage so that four fit on a CU
+            TA_LAUNCH((seg_tile_kernel<D, FP16, 1, 1, 1>), dim3(sp.n_items), dim3(64), stream, sp);
+            break;
+        case TA_TAIL:  // as TA_SMALL, merging the request into out when out is given
+            if (sp.out) return launch_tail_merge<D, FP16>(sp, stream);
             TA_LAUNCH((seg_tile_kernel<D, FP16, 1, 1, 1>), dim3(sp.n_items), dim3(64), stream, sp);
             break;
         case TA_LARGE64:
@@ -365,7 +817,7 @@ hipError_t launch_d(const SegParams &sp, int kind, hipStream_t stream) {
             TA_LAUNCH((seg_tile_kernel<D, FP16, 2, 4, 3>), dim3(sp.n_items), dim3(256), stream, sp);
             break;
         case TA_LARGE256:
-            TA_LAUNCH((seg_tile_kernel<D, FP16, 2, 8, 3>), dim3(sp.n_items), dim3(512), stream, sp);
+            TA_LAUNCH((seg_pipe_kernel<D, FP16, 8>), dim3(sp.n_items), dim3(512), stream, sp);
             break;
         default:
             return hipErrorNotSupported;

@@ -86,6 +86,11 @@ struct SegParams {
     float *part, *lse;
     int n_items, hq, hk, group, tcap, maxr;
     float scale_log2;  // log2(e) / sqrt(D)
+    // TA_TAIL items with a fused merge (out != nullptr): the request's partial
+    // slots and the output
+    const int32_t *slots, *counts;
+    u16 *out;
+    int maxs;
 };
 
 // Kernel timing hook (ta_time_next_launch): when set, the next kernel this

@@ -445,12 +445,13 @@ constexpr int MERGE_CHUNK = 8;
 template <int D, bool FP16>
 __global__ __launch_bounds__(NT) void merge_kernel(const float *__restrict__ part, const float *__restrict__ lse,
                                                    const int32_t *__restrict__ slots,
-                                                   const int32_t *__restrict__ counts, u16 *__restrict__ out,
+                                                   const int32_t *__restrict__ counts,
+                                                   const int32_t *__restrict__ reqs, u16 *__restrict__ out,
                                                    int hq, int maxs) {
     constexpr int TPH = D / 4;    // threads per head
     constexpr int MH = NT / TPH;  // heads per workgroup
     constexpr float LOG2E = 1.44269504088896341f;
-    const int r = blockIdx.x;
+    const int r = reqs ? reqs[blockIdx.x] : blockIdx.x;
     const int tid = threadIdx.x;
     const int hl = tid / TPH, d4 = tid % TPH;
     const int head = blockIdx.y * MH + hl;
@@ -508,7 +509,8 @@ hipError_t launch_segment(const SegParams &sp, int kind, hipStream_t stream) {
     }
 #endif
     switch (kind) {
-        case TA_SMALL: {
+        case TA_SMALL:
+        case TA_TAIL: {  // the fused merge exists only on the LDS-transpose path
             const int blocks = sp.n_items < SMALL_MAX_BLOCKS ? sp.n_items : SMALL_MAX_BLOCKS;
             TA_LAUNCH((seg_small_kernel<D, FP16>), dim3(blocks), dim3(SMALL_NT), stream, sp);
             break;
@@ -528,12 +530,13 @@ hipError_t launch_segment(const SegParams &sp, int kind, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// nreq requests: reqs[0 .. nreq) when reqs is given, else 0 .. nreq-1
 template <int D, bool FP16>
 hipError_t launch_merge(const float *part, const float *lse, const int32_t *slots, const int32_t *counts,
-                        void *out, int nreq, int hq, int maxs, hipStream_t stream) {
+                        const int32_t *reqs, void *out, int nreq, int hq, int maxs, hipStream_t stream) {
     constexpr int MH = NT / (D / 4);
     TA_LAUNCH((merge_kernel<D, FP16>), dim3(nreq, (hq + MH - 1) / MH), dim3(NT), stream, part,
-                       lse, slots, counts, static_cast<u16 *>(out), hq, maxs);
+                       lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs);
     return hipGetLastError();
 }
 
@@ -571,17 +574,30 @@ const char *ta_error_string(int code) {
     }
 }
 
-int ta_segment(const void *q, const void *kp, const void *vp, const int32_t *qids, const int32_t *kstart,
-               const int32_t *qlen, const int32_t *klen, const int32_t *rowbase, const int32_t *items,
-               int32_t n_items, int32_t kind, float *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
-               int32_t d, int32_t tcap, int32_t maxr, int32_t dtype, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// One segment launch; with out given (TA_TAIL only) the items merge their
+// requests into out.
+int segment_launch(const void *q, const void *kp, const void *vp, const int32_t *qids, const int32_t *kstart,
+                   const int32_t *qlen, const int32_t *klen, const int32_t *rowbase, const int32_t *items,
+                   int32_t n_items, int32_t kind, float *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
+                   int32_t d, int32_t tcap, int32_t maxr, int32_t dtype, const int32_t *slots,
+                   const int32_t *counts, void *out, int32_t maxs, void *stream) {
     if (int e = check_common(hq, hk, d, dtype)) return e;
-    if (n_items < 0 || nreq <= 0 || tcap <= 0 || maxr <= 0 || kind < TA_SMALL || kind > TA_LARGE256)
-        return TA_ERR_ARG;
+    if (n_items < 0 || nreq <= 0 || tcap <= 0 || maxr <= 0 || kind < TA_SMALL || kind > TA_TAIL) return TA_ERR_ARG;
     if (n_items == 0) return 0;
     if (!q || !kp || !vp || !qids || !kstart || !qlen || !klen || !rowbase || !items || !part || !lse)
         return TA_ERR_ARG;
     if (!aligned16(q) || !aligned16(kp) || !aligned16(vp) || !aligned16(part)) return TA_ERR_ALIGN;
+    if (out) {
+#ifdef TA_LEGACY_LARGE
+        return TA_ERR_ARG;  // the register-staged kernels have no fused merge
+#endif
+        if (kind != TA_TAIL || tcap % 8 != 0 || !slots || !counts || maxs <= 0) return TA_ERR_ARG;
+        if (!aligned16(out)) return TA_ERR_ALIGN;
+    }
     SegParams sp;
     sp.q = static_cast<const u16 *>(q);
     sp.kp = static_cast<const u16 *>(kp);
@@ -601,10 +617,34 @@ int ta_segment(const void *q, const void *kp, const void *vp, const int32_t *qid
     sp.tcap = tcap;
     sp.maxr = maxr;
     sp.scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)d));
+    sp.slots = slots;
+    sp.counts = counts;
+    sp.out = static_cast<u16 *>(out);
+    sp.maxs = maxs;
     const hipStream_t st = static_cast<hipStream_t>(stream);
 #define TA_SEG(D, F) launch_segment<D, F>(sp, kind, st)
     return (int)TA_DISPATCH(d, dtype == TA_FP16, TA_SEG);
 #undef TA_SEG
+}
+
+int plan_segment(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan, int kind,
+                 void *out, void *stream) {
+    return segment_launch(q, kp, vp, plan->qids, plan->kstart, plan->qlen, plan->klen, plan->rowbase,
+                          plan->items[kind], plan->n_items[kind], kind, plan->part, plan->lse, plan->nreq, plan->hq,
+                          plan->hk, plan->d, tcap, plan->maxr, plan->dtype, plan->slots, plan->counts, out,
+                          plan->maxs, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ta_segment(const void *q, const void *kp, const void *vp, const int32_t *qids, const int32_t *kstart,
+               const int32_t *qlen, const int32_t *klen, const int32_t *rowbase, const int32_t *items,
+               int32_t n_items, int32_t kind, float *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
+               int32_t d, int32_t tcap, int32_t maxr, int32_t dtype, void *stream) {
+    return segment_launch(q, kp, vp, qids, kstart, qlen, klen, rowbase, items, n_items, kind, part, lse, nreq, hq,
+                          hk, d, tcap, maxr, dtype, nullptr, nullptr, nullptr, 0, stream);
 }
 
 int ta_merge(const float *part, const float *lse, const int32_t *slots, const int32_t *counts, void *out,
@@ -614,8 +654,49 @@ int ta_merge(const float *part, const float *lse, const int32_t *slots, const in
     if (!part || !lse || !slots || !counts || !out) return TA_ERR_ARG;
     if (!aligned16(part) || !aligned16(out)) return TA_ERR_ALIGN;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-#define TA_MRG(D, F) launch_merge<D, F>(part, lse, slots, counts, out, nreq, hq, maxs, st)
+#define TA_MRG(D, F) launch_merge<D, F>(part, lse, slots, counts, nullptr, out, nreq, hq, maxs, st)
     return (int)TA_DISPATCH(d, dtype == TA_FP16, TA_MRG);
+#undef TA_MRG
+}
+
+int ta_tail_merge(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan, void *out,
+                  void *stream) {
+    if (!plan || !out || tcap % 8 != 0) return TA_ERR_ARG;
+    return plan_segment(q, kp, vp, tcap, plan, TA_TAIL, out, stream);
+}
+
+int ta_attention_matrix(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan,
+                        void *out, void *stream) {
+    if (!plan || !out) return TA_ERR_ARG;
+#ifdef TA_LEGACY_LARGE
+    const bool fused = false;
+#else
+    const bool fused = tcap % 8 == 0;  // the LDS-transpose kernels carry the fused merge
+#endif
+    // the partials every merge reads come first: large jobs, then small jobs
+    static const int order[] = {TA_LARGE256, TA_LARGE128, TA_LARGE64, TA_SMALL};
+    for (int kind : order) {
+        if (plan->n_items[kind] == 0) continue;
+        if (int e = plan_segment(q, kp, vp, tcap, plan, kind, nullptr, stream)) return e;
+    }
+    if (!fused) {
+        if (plan->n_items[TA_TAIL] > 0)
+            if (int e = plan_segment(q, kp, vp, tcap, plan, TA_TAIL, nullptr, stream)) return e;
+        return ta_merge(plan->part, plan->lse, plan->slots, plan->counts, out, plan->nreq, plan->hq, plan->d,
+                        plan->maxs, plan->dtype, stream);
+    }
+    if (plan->n_items[TA_TAIL] > 0)
+        if (int e = plan_segment(q, kp, vp, tcap, plan, TA_TAIL, out, stream)) return e;
+    if (plan->n_rest <= 0) return 0;
+    if (!plan->rest || !plan->part || !plan->lse || !plan->slots || !plan->counts) return TA_ERR_ARG;
+    if (plan->dtype != TA_BF16 && plan->dtype != TA_FP16) return TA_ERR_DTYPE;
+    if (plan->maxs <= 0 || (plan->d != 32 && plan->d != 64 && plan->d != 128)) return TA_ERR_ARG;
+    if (!aligned16(plan->part) || !aligned16(out)) return TA_ERR_ALIGN;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+#define TA_MRG(D, F) \
+    launch_merge<D, F>(plan->part, plan->lse, plan->slots, plan->counts, plan->rest, out, plan->n_rest, plan->hq, \
+                       plan->maxs, st)
+    return (int)TA_DISPATCH(plan->d, plan->dtype == TA_FP16, TA_MRG);
 #undef TA_MRG
 }
 
@@ -623,21 +704,6 @@ int ta_time_next_launch(void *start_event, void *stop_event) {
     if ((start_event == nullptr) != (stop_event == nullptr)) return TA_ERR_ARG;
     ta::g_launch_events = ta::LaunchEvents{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
     return 0;
-}
-
-int ta_attention_matrix(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan,
-                        void *out, void *stream) {
-    if (!plan) return TA_ERR_ARG;
-    for (int kind = TA_SMALL; kind <= TA_LARGE256; ++kind) {
-        const int n = plan->n_items[kind];
-        if (n == 0) continue;
-        const int e = ta_segment(q, kp, vp, plan->qids, plan->kstart, plan->qlen, plan->klen, plan->rowbase,
-                                 plan->items[kind], n, kind, plan->part, plan->lse, plan->nreq, plan->hq,
-                                 plan->hk, plan->d, tcap, plan->maxr, plan->dtype, stream);
-        if (e) return e;
-    }
-    return ta_merge(plan->part, plan->lse, plan->slots, plan->counts, out, plan->nreq, plan->hq, plan->d,
-                    plan->maxs, plan->dtype, stream);
 }
 
 }  // extern "C"

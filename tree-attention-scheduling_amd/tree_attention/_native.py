@@ -16,14 +16,15 @@ from pathlib import Path
 LIB_PATH = Path(__file__).with_name("libtree_attn.so")
 
 TA_BF16, TA_FP16 = 0, 1
-TA_SMALL, TA_LARGE64, TA_LARGE128, TA_LARGE256 = 0, 1, 2, 3
+TA_SMALL, TA_LARGE64, TA_LARGE128, TA_LARGE256, TA_TAIL = 0, 1, 2, 3, 4
+TA_NKINDS = 5
 KIND_ROWS = {TA_LARGE64: 64, TA_LARGE128: 128, TA_LARGE256: 256}
 
 _c_i32 = ctypes.c_int32
 _c_ptr = ctypes.c_void_p
 
 EXPORTS = ("ta_version", "ta_error_string", "ta_segment", "ta_merge", "ta_attention_matrix",
-           "ta_time_next_launch")
+           "ta_tail_merge", "ta_time_next_launch")
 
 
 class TaPlan(ctypes.Structure):
@@ -31,10 +32,10 @@ class TaPlan(ctypes.Structure):
     _fields_ = [
         ("qids", _c_ptr), ("kstart", _c_ptr), ("qlen", _c_ptr), ("klen", _c_ptr),
         ("rowbase", _c_ptr), ("slots", _c_ptr), ("counts", _c_ptr),
-        ("items", _c_ptr * 4), ("n_items", _c_i32 * 4),
+        ("items", _c_ptr * TA_NKINDS), ("n_items", _c_i32 * TA_NKINDS), ("rest", _c_ptr),
         ("part", _c_ptr), ("lse", _c_ptr),
         ("njobs", _c_i32), ("maxr", _c_i32), ("maxs", _c_i32), ("nreq", _c_i32), ("nslot", _c_i32),
-        ("hq", _c_i32), ("hk", _c_i32), ("d", _c_i32), ("dtype", _c_i32),
+        ("hq", _c_i32), ("hk", _c_i32), ("d", _c_i32), ("dtype", _c_i32), ("n_rest", _c_i32),
     ]
 
 
@@ -71,6 +72,8 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         lib.ta_attention_matrix.restype = ctypes.c_int
         lib.ta_attention_matrix.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_i32, ctypes.POINTER(TaPlan),
                                             _c_ptr, _c_ptr]
+        lib.ta_tail_merge.restype = ctypes.c_int
+        lib.ta_tail_merge.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_i32, ctypes.POINTER(TaPlan), _c_ptr, _c_ptr]
         lib.ta_time_next_launch.restype = ctypes.c_int
         lib.ta_time_next_launch.argtypes = [_c_ptr, _c_ptr]
         if path is None:

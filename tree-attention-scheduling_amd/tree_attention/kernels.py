@@ -68,19 +68,35 @@ class PreparedPlan:
     items: dict = field(default_factory=dict)
     abi: _native.TaPlan | None = None
     metadata: torch.Tensor | None = None
+    rest: torch.Tensor | None = None  # requests the merge kernel covers (no TA_TAIL job)
 
 
-def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256):
+def _tail_jobs(jobs, small_jobs):
+    """Indices of the small jobs that are the only small job of their one request.
+
+    Their work items (kind TA_TAIL) also merge that request's partials, so the
+    merge kernel covers only the other requests.
+    """
+    owners = {}
+    for j in range(small_jobs):
+        for r in jobs[j].requests:
+            owners[r] = owners.get(r, 0) + 1
+    return {j for j in range(small_jobs) if len(jobs[j].requests) == 1 and owners[jobs[j].requests[0]] == 1}
+
+
+def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256, tails=frozenset()):
     """Work-item triples ``(job, first row, KV head)`` per kernel kind as int32 arrays.
 
-    Small jobs (<= 16 query rows) get one item per KV head; larger jobs one per
-    (row tile, KV head), the tile size chosen by ``_large_kind``.
+    Small jobs (<= 16 query rows) get one item per KV head, of kind TA_TAIL for
+    the jobs in ``tails`` and TA_SMALL otherwise; larger jobs one per (row
+    tile, KV head), the tile size chosen by ``_large_kind``.
     """
-    triples = {k: [] for k in (_native.TA_SMALL, *_native.KIND_ROWS)}
+    triples = {k: [] for k in (_native.TA_SMALL, *_native.KIND_ROWS, _native.TA_TAIL)}
     for j in range(len(jobs)):
         rows = len(jobs[j].requests) * group
         if j < small_jobs:
-            triples[_native.TA_SMALL].extend((j, 0, h) for h in range(kvheads))
+            kind = _native.TA_TAIL if j in tails else _native.TA_SMALL
+            triples[kind].extend((j, 0, h) for h in range(kvheads))
             continue
         kind = _large_kind(rows, tile_rows)
         tile = _native.KIND_ROWS[kind]
@@ -93,19 +109,19 @@ def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256):
 TOKEN_QUANTUM = 64  # tokens per LDS tile of the segment kernels
 
 
-def _recut(jobs, items_per_chunk, target_items, fixed_from):
+def _recut(jobs, items_per_chunk, target_items, is_fixed):
     """Execution jobs for one kernel kind: runs of consecutive jobs over the same
     requests and contiguous tokens are cut again into near-equal chunks, as long
     as possible while the kind still gets ``target_items`` work items (one
     workgroup per CU for the large kinds).  Fewer, longer chunks mean fewer
     partial outputs to write and merge; the result is the same attention.
-    Jobs whose tokens start at or after ``fixed_from`` (growing decode tails)
-    are left alone.
+    Jobs for which ``is_fixed(job)`` holds (growing decode tails, tails that
+    merge their request) are left alone.
     """
     runs = []  # [requests, first token, length, fixed]
     for job in jobs:
         t0, n = job.tokens[0], len(job.tokens)
-        fixed = fixed_from is not None and t0 >= fixed_from
+        fixed = is_fixed(job)
         last = runs[-1] if runs else None
         if last and not fixed and not last[3] and last[0] == job.requests and last[1] + last[2] == t0:
             last[2] += n
@@ -171,9 +187,21 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     small = [j for j in jobs if len(j.requests) * group <= SMALL_ROWS]
     large = [j for j in jobs if len(j.requests) * group > SMALL_ROWS]
     n_cu = _cu_count(q.device)
-    small = _recut(small, lambda r: kvheads, 8 * n_cu, fixed_from)
+
+    def growing(job):
+        return fixed_from is not None and job.tokens[0] >= fixed_from
+
+    # Tails (a request's only small job) stay whole when they alone fill the GPU,
+    # so that their work items can merge their requests.
+    owners = {}
+    for j in small:
+        for r in j.requests:
+            owners[r] = owners.get(r, 0) + 1
+    tails = [j for j in small if len(j.requests) == 1 and owners[j.requests[0]] == 1]
+    keep = {id(j) for j in tails} if len(tails) * kvheads >= n_cu else set()
+    small = _recut(small, lambda r: kvheads, 8 * n_cu, lambda j: growing(j) or id(j) in keep)
     large = _recut(large, lambda r: -(-len(r) * group // _native.KIND_ROWS[_large_kind(len(r) * group, tile_rows)])
-                   * kvheads, n_cu, fixed_from)
+                   * kvheads, n_cu, growing)
     jobs = small + large
     small_jobs = len(small)
     njobs = len(jobs)
@@ -197,22 +225,29 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
                 raise ValueError(f"Job {i} names request {r} outside q's {nreq} requests")
             slots[r].append(nslot + local)
         nslot += len(reqs)
+    tails = _tail_jobs(jobs, small_jobs)
+    for j in tails:  # a tail job's slot goes last: its work item merges the others first
+        r, own = jobs[j].requests[0], int(rowbase[j])
+        slots[r].remove(own)
+        slots[r].append(own)
     maxs = max(1, max(map(len, slots)))
     slot_array = np.zeros((nreq, maxs), dtype=np.int32)
     for r, values in enumerate(slots):
         slot_array[r, :len(values)] = values
     counts = np.array([len(s) for s in slots], dtype=np.int32)
-    items = _build_items(jobs, small_jobs, group, kvheads, tile_rows)
+    items = _build_items(jobs, small_jobs, group, kvheads, tile_rows, tails)
+    tail_requests = {jobs[j].requests[0] for j in tails}
+    rest = np.array([r for r in range(nreq) if r not in tail_requests], dtype=np.int32)
 
-    arrays = [qids, kids, qlen, klen, slot_array, counts, rowbase] + [items[k] for k in sorted(items)]
+    arrays = [qids, kids, qlen, klen, slot_array, counts, rowbase, rest] + [items[k] for k in sorted(items)]
     dev = q.device
     metadata = torch.from_numpy(np.concatenate([a.ravel() for a in arrays])).to(dev)
     views, offset = [], 0
     for array in arrays:
         views.append(metadata[offset:offset + array.size].view(array.shape))
         offset += array.size
-    qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t = views[:7]
-    item_views = dict(zip(sorted(items), views[7:]))
+    qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t, rest_t = views[:8]
+    item_views = dict(zip(sorted(items), views[8:]))
     contiguous_q = all(j.requests[-1] - j.requests[0] + 1 == len(j.requests) for j in jobs)
     part = torch.empty((nslot, hq, dim), device=dev, dtype=torch.float32)
     lse = torch.empty((nslot, hq), device=dev, dtype=torch.float32)
@@ -225,12 +260,13 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     for kind, view in item_views.items():
         abi.items[kind] = view.data_ptr() if view.numel() else None
         abi.n_items[kind] = view.numel() // 3
+    abi.rest, abi.n_rest = (rest_t.data_ptr() if rest.size else None), int(rest.size)
     abi.part, abi.lse = part.data_ptr(), lse.data_ptr()
     abi.njobs, abi.maxr, abi.maxs, abi.nreq, abi.nslot = njobs, maxr, maxs, nreq, nslot
     abi.hq, abi.hk, abi.d = hq, kvheads, dim
     abi.dtype = _DTYPES.get(q.dtype, -1)
     return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
-                        slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata)
+                        slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t)
 
 
 def pack_kv(k: torch.Tensor, v: torch.Tensor):
@@ -281,7 +317,10 @@ def attention_matrix(q, kp, vp, prepared):
 
 
 def segment(q, kp, vp, prepared, kind: int):
-    """Launch one segment phase (``kind`` = TA_SMALL / TA_LARGE64/128/256) of a plan.
+    """Launch one segment phase (``kind`` = TA_SMALL / TA_LARGE64/128/256 / TA_TAIL) of a plan.
+
+    Every kind writes partials here, TA_TAIL included; ``merge`` then combines
+    all requests.
 
     Counterpart of the direct ``_segment`` launches in the reference's
     scripts/calibrate_tiles.py:24-29 and scripts/profile_kernel.py:17-20.
@@ -299,6 +338,23 @@ def segment(q, kp, vp, prepared, kind: int):
                             abi.qlen, abi.klen, abi.rowbase, abi.items[kind], n, kind, abi.part, abi.lse,
                             abi.nreq, abi.hq, abi.hk, abi.d, kp.shape[2], abi.maxr, abi.dtype, stream)
     _native.check(rc)
+
+
+def tail_merge(q, kp, vp, prepared):
+    """Launch the fused tail-and-merge kind of a plan (``ta_tail_merge``) into ``prepared.out``.
+
+    Each TA_TAIL item attends its request's tail job and merges the request's
+    other partial slots, which earlier ``segment`` launches on the stream wrote.
+    """
+    p = prepared
+    _check_inputs(q, kp, vp, p)
+    lib = _native.load()
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.ta_tail_merge(q.contiguous().data_ptr(), kp.data_ptr(), vp.data_ptr(), kp.shape[2],
+                               ctypes.byref(p.abi), p.out.data_ptr(), stream)
+    _native.check(rc)
+    return p.out
 
 
 def merge(prepared):

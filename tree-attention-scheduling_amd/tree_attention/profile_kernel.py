@@ -4,7 +4,8 @@
         --cost-model mi355x --kernel large256 --iters 20
 
 ``--kernel`` is one of ``small``, ``large64``, ``large128``, ``large256``,
-``merge``, ``layer`` (the whole attention_matrix call) or ``copy`` (a plain
+``tail`` (the tail items writing partials), ``tailmerge`` (the same items
+merging their requests, as in the layer), ``merge``, ``layer`` (the whole attention_matrix call) or ``copy`` (a plain
 device-to-device copy of ``--copy-mib`` MiB, the reference point that scales
 rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes).  K/V rotate over
 ``--pools`` copies so repeated launches read HBM, not the MALL.  Prints the
@@ -19,18 +20,20 @@ import torch
 
 from . import CostModel, schedule, shapes
 from . import _native
-from .kernels import attention_matrix, merge, pack_kv, prepare, segment
+from .kernels import attention_matrix, merge, pack_kv, prepare, segment, tail_merge
 
 KINDS = {"small": _native.TA_SMALL, "large64": _native.TA_LARGE64, "large128": _native.TA_LARGE128,
-         "large256": _native.TA_LARGE256}
+         "large256": _native.TA_LARGE256, "tail": _native.TA_TAIL}
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--shape", default="wide_long")
+    ap.add_argument("--shared-prefix", default=None, metavar="R,ROOT,PRIVATE",
+                    help="instead of --shape: R requests on one ROOT-token root with PRIVATE-token tails")
     ap.add_argument("--method", default="cube")
     ap.add_argument("--cost-model", default="mi355x", choices=["mi355x", "reference"])
-    ap.add_argument("--kernel", default="layer", choices=sorted(KINDS) + ["merge", "layer", "copy"])
+    ap.add_argument("--kernel", default="layer", choices=sorted(KINDS) + ["tailmerge", "merge", "layer", "copy"])
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--pools", type=int, default=8)
@@ -40,7 +43,12 @@ def main(argv=None):
                     help="CostModel field override, e.g. --param kv_split=1024 (repeatable)")
     args = ap.parse_args(argv)
     hq, hk, d = map(int, args.heads.split(","))
-    spec = shapes.benchmark_cases()[args.shape]
+    if args.shared_prefix:
+        r, root, private = map(int, args.shared_prefix.split(","))
+        spec = shapes.shared_prefix(r, root, private)
+        args.shape = f"shared_prefix({r},{root},{private})"
+    else:
+        spec = shapes.benchmark_cases()[args.shape]
     tree = shapes.tree(spec)
     model = CostModel.mi355x() if args.cost_model == "mi355x" else CostModel()
     for kv in args.param:
@@ -68,6 +76,8 @@ def main(argv=None):
             attention_matrix(q, kpi, vpi, prepared)
         elif args.kernel == "merge":
             merge(prepared)
+        elif args.kernel == "tailmerge":
+            tail_merge(q, kpi, vpi, prepared)
         else:
             segment(q, kpi, vpi, prepared, KINDS[args.kernel])
 
