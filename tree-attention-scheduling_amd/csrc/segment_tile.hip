@@ -641,95 +641,64 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
 
 // ------------------------------------------------------------------------
 // Tail kernel with the merge fused in (TA_TAIL items with out given).  One
-// wave per (tail job, KV head): the job's single request has G = hq/hk query
-// rows for this head, and every other partial slot of the request was written
-// by an earlier launch on the stream.  The wave
-//   1. starts the DMA of the tail's first K/V tile, the loads of the first
-//      PF / UPL other slots (o and lse; the job's own slot is the request's
-//      last) and the Q loads, so that the three latencies overlap;
-//   2. attends the tail (the small-job tile loop);
-//   3. puts its own normalised partial and log-sum-exp in LDS, re-read in the
-//      merge layout: lane l owns units u = l + 64k (k < UPL) of G*D/4 float4
-//      units, unit u = (row u / (D/4), d = 4 (u % (D/4)));
-//   4. merges the own partial with the other slots by the online log-sum-exp
-//      of the merge kernel and writes the output rows.
+// two-wave workgroup per (tail job, KV head): the job's single request has
+// G = hq/hk query rows for this head, and every other partial slot of the
+// request was written by an earlier launch on the stream (the job's own slot
+// is the request's last).  The two waves work side by side:
+//   wave 0 attends the tail (the small-job tile loop) and leaves its
+//          normalised partial and log-sum-exp in LDS;
+//   wave 1 loads the other slots, PF float4 registers per round, and merges
+//          them by the online log-sum-exp of the merge kernel; lane l owns
+//          units u = l + 64k (k < UPL) of the G*D/4 float4 units, unit u =
+//          (row u / (D/4), d = 4 (u % (D/4))).
+// After one barrier wave 1 merges the own partial and writes the output rows.
 template <int D, bool FP16, int UPL>
-__global__ __launch_bounds__(64) void seg_tail_kernel(SegParams p) {
+__global__ __launch_bounds__(128) void seg_tail_kernel(SegParams p) {
     using T = Tile<D>;
     using M = TileMath<D, FP16, 1, 1>;
     constexpr int KS = M::KS, DB = M::DB;
-    constexpr int PF = 32;          // float4 registers of prefetched slots
+    constexpr int PF = 32;          // float4 registers of one merge round
     constexpr int CH = PF / UPL;    // slots per merge round
     constexpr int DU = D / 4;       // units per row
     constexpr float LOG2E = 1.44269504088896341f;
     __shared__ __attribute__((aligned(16))) u16 lds[T::ELEMS];
+    float *opart = reinterpret_cast<float *>(lds);  // [G][D] own normalised partial, after the tile loop
+    float *olse = opart + 16 * D;                   // [G] own log-sum-exp, log2 units
 
     const int item = blockIdx.x;
     const int job = p.items[3 * item], h = p.items[3 * item + 2];
-    const int lane = threadIdx.x;
-    const int row = lane & 15, g4 = lane >> 4;
-    const int kst = p.kstart[job];
-    const int ntok = max(0, min(p.klen[job], p.tcap - kst));
-    const int kend = kst + ntok;
-    const int G = p.group;  // rows of the job (one request)
-    const int tb0 = kst & ~7;
-    const int ntiles = ntok > 0 ? (kend - tb0 + T::TT - 1) / T::TT : 0;
+    const int G = p.group;
+    const int lane = threadIdx.x & 63;
     const int r = p.qids[(size_t)job * p.maxr];
-    const int own = p.rowbase[job];
-    const int cnt = p.counts[r] - 1;  // other slots; the job's own slot is the last one
-    const int32_t *slr = p.slots + (size_t)r * p.maxs;
-    const int units = G * DU;
 
-    // 1. first tile, first merge round, Q
-    if (ntiles > 0) M::copy(lds, p.kp, p.vp, h, p.tcap, tb0, kst, kend, 0, lane);
-    float l[CH][UPL];
-    f32x4 v[CH][UPL];
-    auto load_round = [&](int s0) {
+    if (threadIdx.x < 64) {
+        // ---- wave 0: the tail's attention
+        const int row = lane & 15, g4 = lane >> 4;
+        const int kst = p.kstart[job];
+        const int ntok = max(0, min(p.klen[job], p.tcap - kst));
+        const int kend = kst + ntok;
+        const int tb0 = kst & ~7;
+        const int ntiles = ntok > 0 ? (kend - tb0 + T::TT - 1) / T::TT : 0;
+        if (ntiles > 0) M::copy(lds, p.kp, p.vp, h, p.tcap, tb0, kst, kend, 0, lane);
+        u32x4 qf[1][KS];
+        {
+            const int rr = row < G ? row : 0;  // rows past G repeat row 0 and are never stored
+            const u16 *src = p.q + ((size_t)r * p.hq + h * G + rr) * D + 8 * g4;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int si = s0 + c;
-            const int sl = slr[min(si, max(cnt - 1, 0))];
-            const bool use = si < cnt && sl != own;
-#pragma unroll
-            for (int k = 0; k < UPL; ++k) {
-                const int u = min(lane + 64 * k, units - 1);
-                const int head = h * G + u / DU;
-                const size_t prow = (size_t)sl * p.hq + head;
-                const f32x4 x = *(const f32x4 *)(p.part + prow * D + 4 * (u % DU));
-                const float lx = p.lse[prow];
-                // the own slot's row is not written on this path: keep it out
-                l[c][k] = use ? lx * LOG2E : NEG_INF;
-                v[c][k] = use ? x : f32x4{0.f, 0.f, 0.f, 0.f};
-            }
+            for (int k = 0; k < KS; ++k) qf[0][k] = *(const u32x4 *)(src + 32 * k);
         }
-    };
-    load_round(0);
-    u32x4 qf[1][KS];
-    {
-        const int rr = row < G ? row : 0;  // rows past G duplicate row 0; never stored
-        const u16 *src = p.q + ((size_t)r * p.hq + h * G + rr) * D + 8 * g4;
-#pragma unroll
-        for (int k = 0; k < KS; ++k) qf[0][k] = *(const u32x4 *)(src + 32 * k);
-    }
-
-    // 2. attend the tail
-    M acc;
-    acc.reset();
-    const int lane_ofs = 8 * (4 * ((row & 3) >> 1) + (row >> 2)) + 4 * (row & 1);
-    const int koff = T::BLK * g4 + lane_ofs;
-    const int voff = T::BLK * ((4 * g4) / T::VROWS) + 64 * (((4 * g4) % T::VROWS) >> 2) + lane_ofs;
-    for (int it = 0; it < ntiles; ++it) {
-        const int t0 = tb0 + it * T::TT;
-        if (it > 0) M::copy(lds, p.kp, p.vp, h, p.tcap, t0, kst, kend, 0, lane);
-        __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
-        acc.tile(lds, qf, koff, voff, max(0, kst - t0), min(T::TT, kend - t0), g4, p.scale_log2);
-    }
-
-    // 3. own partial through LDS into the merge layout (the tile stage is free:
-    //    its reads fed the MFMAs above)
-    float *opart = reinterpret_cast<float *>(lds);  // [G][D] normalised partial
-    float *olse = opart + 16 * D;                   // [G] log-sum-exp, log2 units
-    {
+        M acc;
+        acc.reset();
+        const int lane_ofs = 8 * (4 * ((row & 3) >> 1) + (row >> 2)) + 4 * (row & 1);
+        const int koff = T::BLK * g4 + lane_ofs;
+        const int voff = T::BLK * ((4 * g4) / T::VROWS) + 64 * (((4 * g4) % T::VROWS) >> 2) + lane_ofs;
+        for (int it = 0; it < ntiles; ++it) {
+            const int t0 = tb0 + it * T::TT;
+            if (it > 0) M::copy(lds, p.kp, p.vp, h, p.tcap, t0, kst, kend, 0, lane);
+            __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
+            acc.tile(lds, qf, koff, voff, max(0, kst - t0), min(T::TT, kend - t0), g4, p.scale_log2);
+        }
+        // the tile's reads fed the MFMAs above, so the stage is free for the partial
         const bool any = acc.m[0] != NEG_INF;
         const float zr = acc.z[0][0];
         const float inv = any ? 1.f / zr : 0.f;
@@ -739,20 +708,41 @@ __global__ __launch_bounds__(64) void seg_tail_kernel(SegParams p) {
                 *(f32x4 *)(opart + row * D + 16 * db + 4 * g4) = acc.o[0][db] * inv;
             if (g4 == 0) olse[row] = any ? acc.m[0] + __builtin_amdgcn_logf(zr) : NEG_INF;
         }
+        __syncthreads();
+        return;
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
+
+    // ---- wave 1: merge the request's other slots
+    const int own = p.rowbase[job];
+    const int cnt = p.counts[r] - 1;
+    const int32_t *slr = p.slots + (size_t)r * p.maxs;
+    const int units = G * DU;
     float Mx[UPL], Z[UPL];
     f32x4 o[UPL];
 #pragma unroll
     for (int k = 0; k < UPL; ++k) {
-        const int u = min(lane + 64 * k, units - 1);
-        Mx[k] = olse[u / DU];
-        Z[k] = Mx[k] == NEG_INF ? 0.f : 1.f;
-        o[k] = *(const f32x4 *)(opart + (u / DU) * D + 4 * (u % DU));
+        Mx[k] = NEG_INF;
+        Z[k] = 0.f;
+        o[k] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-
-    // 4. merge the other slots, CH per round
-    for (int s0 = 0;;) {
+    for (int s0 = 0; s0 < cnt; s0 += CH) {
+        float l[CH][UPL];
+        f32x4 v[CH][UPL];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int si = s0 + c;
+            const int sl = slr[min(si, cnt - 1)];
+            const bool use = si < cnt && sl != own;
+#pragma unroll
+            for (int k = 0; k < UPL; ++k) {
+                const int u = min(lane + 64 * k, units - 1);
+                const size_t prow = (size_t)sl * p.hq + h * G + u / DU;
+                const f32x4 x = *(const f32x4 *)(p.part + prow * D + 4 * (u % DU));
+                const float lx = p.lse[prow];
+                l[c][k] = use ? lx * LOG2E : NEG_INF;
+                v[c][k] = use ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
 #pragma unroll
         for (int k = 0; k < UPL; ++k) {
             float cm = Mx[k];
@@ -769,15 +759,19 @@ __global__ __launch_bounds__(64) void seg_tail_kernel(SegParams p) {
                 o[k] += w * v[c][k];
             }
         }
-        s0 += CH;
-        if (s0 >= cnt) break;
-        load_round(s0);
     }
+    __syncthreads();  // wave 0's partial is in LDS
 #pragma unroll
     for (int k = 0; k < UPL; ++k) {
         const int u = lane + 64 * k;
         if (u >= units) continue;
-        const f32x4 a = o[k] * (Z[k] > 0.f ? 1.f / Z[k] : 0.f);
+        const float lo = olse[u / DU];
+        const f32x4 vo = *(const f32x4 *)(opart + (u / DU) * D + 4 * (u % DU));
+        const float cm = fmaxf(Mx[k], lo);
+        const float alpha = Mx[k] == NEG_INF ? 0.f : fast_exp2(Mx[k] - cm);
+        const float w = lo == NEG_INF ? 0.f : fast_exp2(lo - cm);
+        const float zt = Z[k] * alpha + w;
+        const f32x4 a = (o[k] * alpha + w * vo) * (zt > 0.f ? 1.f / zt : 0.f);
         u16 *dst = p.out + ((size_t)r * p.hq + h * G + u / DU) * D + 4 * (u % DU);
         *(u32x2 *)dst = u32x2{Ops<FP16>::pack(a[0], a[1]), Ops<FP16>::pack(a[2], a[3])};
     }
@@ -788,13 +782,13 @@ hipError_t launch_tail_merge(const SegParams &sp, hipStream_t stream) {
     // float4 units per lane: G*D/4 units over 64 lanes
     const int units = sp.group * (D / 4);
     if (units <= 64)
-        TA_LAUNCH((seg_tail_kernel<D, FP16, 1>), dim3(sp.n_items), dim3(64), stream, sp);
+        TA_LAUNCH((seg_tail_kernel<D, FP16, 1>), dim3(sp.n_items), dim3(128), stream, sp);
     else if (units <= 128)
-        TA_LAUNCH((seg_tail_kernel<D, FP16, 2>), dim3(sp.n_items), dim3(64), stream, sp);
+        TA_LAUNCH((seg_tail_kernel<D, FP16, 2>), dim3(sp.n_items), dim3(128), stream, sp);
     else if (units <= 256)
-        TA_LAUNCH((seg_tail_kernel<D, FP16, 4>), dim3(sp.n_items), dim3(64), stream, sp);
+        TA_LAUNCH((seg_tail_kernel<D, FP16, 4>), dim3(sp.n_items), dim3(128), stream, sp);
     else if (units <= 512)
-        TA_LAUNCH((seg_tail_kernel<D, FP16, 8>), dim3(sp.n_items), dim3(64), stream, sp);
+        TA_LAUNCH((seg_tail_kernel<D, FP16, 8>), dim3(sp.n_items), dim3(128), stream, sp);
     else
         return hipErrorNotSupported;
     return hipGetLastError();
