@@ -12,15 +12,18 @@
  *   - Launches are asynchronous on `stream` (a hipStream_t; NULL = default stream).
  *   - Return value: 0 on success, a HIP error code from the launch, or one of the
  *     TA_ERR_* argument errors below.  ta_error_string() names any of them.
- *   - dtype: TA_BF16 or TA_FP16, shared by q, kp, vp and out.  Accumulation, the
- *     partial outputs and the log-sum-exp values are fp32.
+ *   - dtype: TA_BF16 or TA_FP16, shared by q, kp, vp and out.  Accumulation and
+ *     the log-sum-exp values are fp32; partial outputs are stored as fp16 rows
+ *     scaled by a power of two (below).
  *   - Layouts (row-major, contiguous, base 16-byte aligned):
  *       q     [nreq, hq, d]        query of each request (kernels.py:157 permutes it;
  *                                  here the kernel indexes it directly)
  *       kp    [hk, d, tcap]        K pool, token-minor (kernels.py:144, qwen.py:27)
  *       vp    [hk, tcap, d]        V pool                 (kernels.py:145, qwen.py:28)
- *       part  [nslot, hq, d] fp32  normalised partial output per (job, request)
- *       lse   [nslot, hq]    fp32  natural-log log-sum-exp of the same rows
+ *       part  [nslot, hq, d] fp16  normalised partial output per (job, request),
+ *                                  row-scaled: stored value = (o / z) * 2^-e with e
+ *                                  the frexp exponent of the row's largest |o / z|
+ *       lse   [nslot, hq, 2] fp32  per row: natural-log log-sum-exp, then e
  *       out   [nreq, hq, d]
  *   - Job j covers physical tokens [kstart[j], kstart[j] + klen[j]) for the requests
  *     qids[j*maxr + 0 .. qlen[j]-1]; its partial rows are slots rowbase[j] + i.
@@ -70,8 +73,8 @@ typedef struct ta_plan {
     int32_t n_items[TA_NKINDS];       /* number of triples per kind                 */
     const int32_t *rest;      /* [n_rest] requests without a TA_TAIL job: the ones
                                  the merge kernel of ta_attention_matrix covers    */
-    float *part;
-    float *lse;
+    void *part;               /* [nslot, hq, d] fp16, row-scaled                   */
+    float *lse;               /* [nslot, hq, 2]                                    */
     int32_t njobs, maxr, maxs, nreq, nslot;
     int32_t hq, hk, d, dtype;
     int32_t n_rest;
@@ -91,13 +94,13 @@ int ta_segment(const void *q, const void *kp, const void *vp,
                const int32_t *qids, const int32_t *kstart, const int32_t *qlen,
                const int32_t *klen, const int32_t *rowbase,
                const int32_t *items, int32_t n_items, int32_t kind,
-               float *part, float *lse,
+               void *part, float *lse,
                int32_t nreq, int32_t hq, int32_t hk, int32_t d, int32_t tcap,
                int32_t maxr, int32_t dtype, void *stream);
 
 /* Global log-sum-exp merge of each request's partial outputs (replaces _merge,
  * kernels.py:58-83, and its launch at kernels.py:166-167). */
-int ta_merge(const float *part, const float *lse, const int32_t *slots,
+int ta_merge(const void *part, const float *lse, const int32_t *slots,
              const int32_t *counts, void *out, int32_t nreq, int32_t hq,
              int32_t d, int32_t maxs, int32_t dtype, void *stream);
 

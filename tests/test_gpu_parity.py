@@ -216,6 +216,20 @@ def test_attention_packs_and_c_abi_phases_agree(name, device):
     assert relative_l2(b.cpu(), c.cpu().float()) < 5e-4
 
 
+@pytest.mark.parametrize("vscale", [1e5, 1e-5])
+def test_partial_rows_keep_range(vscale, device):
+    """Partial rows are fp16 scaled by 2^-e per row: V far outside fp16's range
+    (or deep in its subnormals) still merges to the FP32 result."""
+    tree = shapes.tree(shapes.benchmark_cases()["wide"])
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 23)
+    v = (v.float() * vscale).bfloat16()
+    ref = oracle_fp32(q, k, v, tree)
+    for method in ("cube", "request"):
+        out = run(tree, method, MI355X_LIKE, q, k, v, device, (32, 8, 128))
+        err = relative_l2(out.cpu(), ref)
+        assert torch.isfinite(out).all() and err <= REL_L2, (method, err)
+
+
 class _Paths:
     def __init__(self, paths):
         self.paths = paths

@@ -41,7 +41,8 @@ def test_metadata_layout_small_first_and_compact_slots():
             slot_owner[rowbase[j] + i] = r
     for r in range(128):
         assert {slot_owner[s] for s in p.slots[r, :counts[r]].tolist()} == {r}
-    assert p.part.shape == (sum(qlen), 32, 128) and p.lse.shape == (sum(qlen), 32)
+    assert p.part.shape == (sum(qlen), 32, 128) and p.lse.shape == (sum(qlen), 32, 2)
+    assert p.part.dtype == torch.float16 and p.lse.dtype == torch.float32
     # work items: one per (small job, head); every private tail is its request's only
     # small job, so all are TA_TAIL items that merge their request and no request is
     # left for the merge kernel; large jobs of 16 requests = 64 rows -> one 64-row tile per head

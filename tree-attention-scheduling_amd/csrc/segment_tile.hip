@@ -342,13 +342,7 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
         if (grow >= nrows) continue;
         const int lr = grow / p.group, gg = grow - lr * p.group;
         const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
-        float *dst = p.part + prow * D + 4 * g4;
-        const bool any = acc.m[nb] != NEG_INF;
-        const float zr = acc.z[nb][0];
-        const float inv = any ? 1.f / zr : 0.f;
-#pragma unroll
-        for (int db = 0; db < M::DB; ++db) *(f32x4 *)(dst + 16 * db) = acc.o[nb][db] * inv;
-        if (g4 == 0) p.lse[prow] = any ? (acc.m[nb] + __builtin_amdgcn_logf(zr)) * LN2 : NEG_INF;
+        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4);
     }
 }
 
@@ -629,13 +623,7 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
         if (grow >= nrows) continue;
         const int lr = grow / p.group, gg = grow - lr * p.group;
         const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
-        float *dst = p.part + prow * D + 4 * g4;
-        const bool any = acc.m[nb] != NEG_INF;
-        const float zr = acc.z[nb][0];
-        const float inv = any ? 1.f / zr : 0.f;
-#pragma unroll
-        for (int db = 0; db < M::DB; ++db) *(f32x4 *)(dst + 16 * db) = acc.o[nb][db] * inv;
-        if (g4 == 0) p.lse[prow] = any ? (acc.m[nb] + __builtin_amdgcn_logf(zr)) * LN2 : NEG_INF;
+        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4);
     }
 }
 
@@ -657,7 +645,7 @@ __global__ __launch_bounds__(128) void seg_tail_kernel(SegParams p) {
     using T = Tile<D>;
     using M = TileMath<D, FP16, 1, 1>;
     constexpr int KS = M::KS, DB = M::DB;
-    constexpr int PF = 32;          // float4 registers of one merge round
+    constexpr int PF = 32;          // units of one merge round
     constexpr int CH = PF / UPL;    // slots per merge round
     constexpr int DU = D / 4;       // units per row
     constexpr float LOG2E = 1.44269504088896341f;
@@ -727,7 +715,8 @@ __global__ __launch_bounds__(128) void seg_tail_kernel(SegParams p) {
     }
     for (int s0 = 0; s0 < cnt; s0 += CH) {
         float l[CH][UPL];
-        f32x4 v[CH][UPL];
+        int e[CH][UPL];
+        u32x2 v[CH][UPL];
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int si = s0 + c;
@@ -737,10 +726,11 @@ __global__ __launch_bounds__(128) void seg_tail_kernel(SegParams p) {
             for (int k = 0; k < UPL; ++k) {
                 const int u = min(lane + 64 * k, units - 1);
                 const size_t prow = (size_t)sl * p.hq + h * G + u / DU;
-                const f32x4 x = *(const f32x4 *)(p.part + prow * D + 4 * (u % DU));
-                const float lx = p.lse[prow];
+                const u32x2 x = *(const u32x2 *)(p.part + prow * D + 4 * (u % DU));
+                const float lx = p.lse[2 * prow], ex = p.lse[2 * prow + 1];
                 l[c][k] = use ? lx * LOG2E : NEG_INF;
-                v[c][k] = use ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+                e[c][k] = (int)ex;
+                v[c][k] = use ? x : u32x2{0u, 0u};
             }
         }
 #pragma unroll
@@ -756,7 +746,7 @@ __global__ __launch_bounds__(128) void seg_tail_kernel(SegParams p) {
             for (int c = 0; c < CH; ++c) {
                 const float w = l[c][k] == NEG_INF ? 0.f : fast_exp2(l[c][k] - cm);
                 Z[k] += w;
-                o[k] += w * v[c][k];
+                o[k] += __builtin_amdgcn_ldexpf(w, e[c][k]) * unpack_f16x4(v[c][k]);
             }
         }
     }

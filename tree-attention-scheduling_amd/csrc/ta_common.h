@@ -79,11 +79,60 @@ __device__ inline float xor_sum(float v) {
     return v + __shfl_xor(v, 32);
 }
 
+// Partial outputs.  Row `prow` (= slot * hq + query head) of a segment's
+// partial output is stored as D fp16 values of (o / z) * 2^-e, where e is the
+// frexp exponent of the row's largest |o / z| (every stored value lies in
+// (-1, 1), whatever the range of V), next to lse2[2 prow] = natural-log
+// log-sum-exp of the row and lse2[2 prow + 1] = e.  Lane (row, g4) of a
+// 16-row MFMA block holds d = 16 db + 4 g4 + i in o[db][i]; the four lanes of
+// a row (g4 = 0..3, lanes 16 apart) must all be active.
+__device__ inline u32 pack_f16(float lo, float hi) {
+    f16x2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(u32, v);
+}
+
+template <int DB>
+__device__ inline void store_partial(u16 *part, float *lse2, size_t prow, const f32x4 (&o)[DB], float m, float z,
+                                     int g4) {
+    constexpr int D = 16 * DB;
+    const bool any = m != NEG_INF;
+    const float inv = any ? 1.f / z : 0.f;
+    float amax = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) amax = fmaxf(amax, __builtin_fabsf(o[db][i]));
+    amax *= inv;
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
+    const float s = __builtin_amdgcn_ldexpf(inv, -e);
+    u16 *dst = part + prow * D + 4 * g4;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        const f32x4 v = o[db] * s;
+        *(u32x2 *)(dst + 16 * db) = u32x2{pack_f16(v[0], v[1]), pack_f16(v[2], v[3])};
+    }
+    if (g4 == 0) {
+        lse2[2 * prow] = any ? (m + __builtin_amdgcn_logf(z)) * LN2 : NEG_INF;
+        lse2[2 * prow + 1] = (float)e;
+    }
+}
+
+// Four fp16 partial values (8 bytes) -> floats.  The whole vector is
+// bit-cast: hipcc (ROCm 7.2) lowers a bit_cast of one element of an
+// ext_vector (w[1]) as if it were element 0.
+__device__ inline f32x4 unpack_f16x4(u32x2 w) {
+    const f16x4 h = __builtin_bit_cast(f16x4, w);
+    return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+
 // Launch arguments of every segment kernel.
 struct SegParams {
     const u16 *q, *kp, *vp;
     const int32_t *qids, *kstart, *qlen, *klen, *rowbase, *items;
-    float *part, *lse;
+    u16 *part;   // [nslot, hq, D] fp16, scaled as above
+    float *lse;  // [nslot, hq, 2]: log-sum-exp and scale exponent
     int n_items, hq, hk, group, tcap, maxr;
     float scale_log2;  // log2(e) / sqrt(D)
     // TA_TAIL items with a fused merge (out != nullptr): the request's partial

@@ -26,8 +26,10 @@
 //     so that tiles of the same (job, head) land on the same XCD back to back
 //     and share its L2.
 //   * Softmax runs in base 2 with log2(e)/sqrt(D) folded into one FMA.
-//   * The merge reads fp32 partials with 16-byte loads, one thread per four
-//     head-dim elements.
+//   * Partial rows are stored as fp16 scaled by a power of two per row (the
+//     exponent sits next to the log-sum-exp); the merge reads them with
+//     8-byte loads, one thread per four head-dim elements, and folds the
+//     scale into each slot's weight.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -276,12 +278,7 @@ __device__ inline void store_rows(const SegParams &p, RowState<D, NB> &st, int j
         if (grow >= nrows) continue;
         const int lr = grow / p.group, gg = grow - lr * p.group;
         const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
-        float *dst = p.part + prow * D + 4 * g4;
-        const bool any = st.m[nb] != NEG_INF;
-        const float inv = any ? 1.f / zr : 0.f;
-#pragma unroll
-        for (int db = 0; db < D / 16; ++db) *(f32x4 *)(dst + 16 * db) = st.o[nb][db] * inv;
-        if (g4 == 0) p.lse[prow] = any ? (st.m[nb] + __builtin_amdgcn_logf(zr)) * LN2 : NEG_INF;
+        store_partial<D / 16>(p.part, p.lse, prow, st.o[nb], st.m[nb], zr, g4);
     }
 }
 
@@ -443,7 +440,7 @@ __global__ __launch_bounds__(64 * NW) void seg_large_kernel(SegParams p) {
 constexpr int MERGE_CHUNK = 8;
 
 template <int D, bool FP16>
-__global__ __launch_bounds__(NT) void merge_kernel(const float *__restrict__ part, const float *__restrict__ lse,
+__global__ __launch_bounds__(NT) void merge_kernel(const u16 *__restrict__ part, const float *__restrict__ lse,
                                                    const int32_t *__restrict__ slots,
                                                    const int32_t *__restrict__ counts,
                                                    const int32_t *__restrict__ reqs, u16 *__restrict__ out,
@@ -458,19 +455,22 @@ __global__ __launch_bounds__(NT) void merge_kernel(const float *__restrict__ par
     if (head >= hq) return;
     const int cnt = counts[r];
     const int32_t *slr = slots + (size_t)r * maxs;
-    const float *src = part + (size_t)head * D + 4 * d4;
+    const u16 *src = part + (size_t)head * D + 4 * d4;
     const size_t srow = (size_t)hq * D;
 
     float M = NEG_INF, Z = 0.f;  // running max (log2 units) and weight sum
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < cnt; s0 += MERGE_CHUNK) {
         float l[MERGE_CHUNK];
+        int e[MERGE_CHUNK];
         f32x4 v[MERGE_CHUNK];
 #pragma unroll
         for (int u = 0; u < MERGE_CHUNK; ++u) {
             const int sl = slr[min(s0 + u, cnt - 1)];
-            l[u] = s0 + u < cnt ? lse[(size_t)sl * hq + head] * LOG2E : NEG_INF;
-            v[u] = *(const f32x4 *)(src + sl * srow);
+            const size_t prow = (size_t)sl * hq + head;
+            l[u] = s0 + u < cnt ? lse[2 * prow] * LOG2E : NEG_INF;
+            e[u] = (int)lse[2 * prow + 1];
+            v[u] = unpack_f16x4(*(const u32x2 *)(src + sl * srow));
         }
         float cm = M;
 #pragma unroll
@@ -486,7 +486,7 @@ __global__ __launch_bounds__(NT) void merge_kernel(const float *__restrict__ par
         for (int u = 0; u < MERGE_CHUNK; ++u) {
             const float w = fast_exp2(l[u] - M);  // 0 for empty slots
             Z += w;
-            acc += w * v[u];
+            acc += __builtin_amdgcn_ldexpf(w, e[u]) * v[u];
         }
     }
     if (Z > 0.f) acc *= 1.f / Z;
@@ -532,11 +532,11 @@ hipError_t launch_segment(const SegParams &sp, int kind, hipStream_t stream) {
 
 // nreq requests: reqs[0 .. nreq) when reqs is given, else 0 .. nreq-1
 template <int D, bool FP16>
-hipError_t launch_merge(const float *part, const float *lse, const int32_t *slots, const int32_t *counts,
+hipError_t launch_merge(const void *part, const float *lse, const int32_t *slots, const int32_t *counts,
                         const int32_t *reqs, void *out, int nreq, int hq, int maxs, hipStream_t stream) {
     constexpr int MH = NT / (D / 4);
-    TA_LAUNCH((merge_kernel<D, FP16>), dim3(nreq, (hq + MH - 1) / MH), dim3(NT), stream, part,
-                       lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs);
+    TA_LAUNCH((merge_kernel<D, FP16>), dim3(nreq, (hq + MH - 1) / MH), dim3(NT), stream,
+              static_cast<const u16 *>(part), lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs);
     return hipGetLastError();
 }
 
@@ -582,7 +582,7 @@ namespace {
 // requests into out.
 int segment_launch(const void *q, const void *kp, const void *vp, const int32_t *qids, const int32_t *kstart,
                    const int32_t *qlen, const int32_t *klen, const int32_t *rowbase, const int32_t *items,
-                   int32_t n_items, int32_t kind, float *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
+                   int32_t n_items, int32_t kind, void *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
                    int32_t d, int32_t tcap, int32_t maxr, int32_t dtype, const int32_t *slots,
                    const int32_t *counts, void *out, int32_t maxs, void *stream) {
     if (int e = check_common(hq, hk, d, dtype)) return e;
@@ -608,7 +608,7 @@ int segment_launch(const void *q, const void *kp, const void *vp, const int32_t 
     sp.klen = klen;
     sp.rowbase = rowbase;
     sp.items = items;
-    sp.part = part;
+    sp.part = static_cast<u16 *>(part);
     sp.lse = lse;
     sp.n_items = n_items;
     sp.hq = hq;
@@ -641,13 +641,13 @@ extern "C" {
 
 int ta_segment(const void *q, const void *kp, const void *vp, const int32_t *qids, const int32_t *kstart,
                const int32_t *qlen, const int32_t *klen, const int32_t *rowbase, const int32_t *items,
-               int32_t n_items, int32_t kind, float *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
+               int32_t n_items, int32_t kind, void *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
                int32_t d, int32_t tcap, int32_t maxr, int32_t dtype, void *stream) {
     return segment_launch(q, kp, vp, qids, kstart, qlen, klen, rowbase, items, n_items, kind, part, lse, nreq, hq,
                           hk, d, tcap, maxr, dtype, nullptr, nullptr, nullptr, 0, stream);
 }
 
-int ta_merge(const float *part, const float *lse, const int32_t *slots, const int32_t *counts, void *out,
+int ta_merge(const void *part, const float *lse, const int32_t *slots, const int32_t *counts, void *out,
              int32_t nreq, int32_t hq, int32_t d, int32_t maxs, int32_t dtype, void *stream) {
     if (dtype != TA_BF16 && dtype != TA_FP16) return TA_ERR_DTYPE;
     if (nreq <= 0 || hq <= 0 || maxs <= 0 || (d != 32 && d != 64 && d != 128)) return TA_ERR_ARG;

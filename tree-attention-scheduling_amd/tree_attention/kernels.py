@@ -249,8 +249,9 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t, rest_t = views[:8]
     item_views = dict(zip(sorted(items), views[8:]))
     contiguous_q = all(j.requests[-1] - j.requests[0] + 1 == len(j.requests) for j in jobs)
-    part = torch.empty((nslot, hq, dim), device=dev, dtype=torch.float32)
-    lse = torch.empty((nslot, hq), device=dev, dtype=torch.float32)
+    # partial rows: fp16 scaled by 2^-e per row; lse holds (log-sum-exp, e) per row
+    part = torch.empty((nslot, hq, dim), device=dev, dtype=torch.float16)
+    lse = torch.empty((nslot, hq, 2), device=dev, dtype=torch.float32)
     out = torch.empty_like(q)
 
     abi = _native.TaPlan()
