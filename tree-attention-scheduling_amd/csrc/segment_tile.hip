@@ -107,29 +107,42 @@ struct TileMath {
     }
 
     // Copy the tile at pool token t0n into stage `st` (this wave's blocks).
+    // Inside the job (tokens [t0n, t0n + TT) all in [kst, kend)) no index is
+    // clamped; at its edges chunks past the pool end read its last chunk and
+    // V rows outside the job read a row inside it (finite values; their
+    // scores are masked, P = 0).
     __device__ static void copy(u16 *st, const u16 *__restrict__ kp, const u16 *__restrict__ vp, int h,
                                 int tcap, int t0n, int kst, int kend, int wave, int lane) {
-        {
+        const int w = __builtin_amdgcn_readfirstlane(wave);
+        if (t0n >= kst && t0n + T::TT <= kend)
+            copy_blocks<false>(st, kp, vp, h, tcap, t0n, kst, kend, w, lane);
+        else
+            copy_blocks<true>(st, kp, vp, h, tcap, t0n, kst, kend, w, lane);
+    }
+
+    template <bool CLAMP>
+    __device__ static void copy_blocks(u16 *st, const u16 *__restrict__ kp, const u16 *__restrict__ vp, int h,
+                                       int tcap, int t0n, int kst, int kend, int w, int lane) {
 #pragma unroll
-            for (int i = 0; i < T::NBLK / NW; ++i) {
-                const int blk = wave + i * NW;
-                const u16 *src;
-                if (blk < T::KBLK) {
-                    const int ck = 2 * (lane >> 4) + ((lane >> 2) & 1);
-                    const int d = 8 * blk + 4 * ((lane >> 3) & 1) + (lane & 3);
-                    // chunks past the pool end read its last chunk; their scores are masked
-                    src = kp + (size_t)(h * D + d) * tcap + min(t0n + 8 * ck, tcap - 8);
-                } else {
-                    const int vb = blk - T::KBLK;
-                    const int rem = lane % T::SV;
-                    const int s = 2 * (lane / T::SV) + ((rem >> 2) & 1);
-                    const int j = 4 * (rem >> 3) + (rem & 3);
-                    // rows outside the job read a row inside it: finite values, P = 0
-                    const int t = min(max(t0n + vb * T::VROWS + j, kst), kend - 1);
-                    src = vp + ((size_t)h * tcap + t) * D + 8 * s;
-                }
-                __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + blk * T::BLK), 16, 0, 0);
+        for (int i = 0; i < T::NBLK / NW; ++i) {
+            const int blk = w + i * NW;
+            // with KBLK % NW == 0 every wave's i-th block is K for the same i
+            const bool isk = T::KBLK % NW == 0 ? i * NW < T::KBLK : blk < T::KBLK;
+            const u16 *src;
+            if (isk) {
+                const int ck = 2 * (lane >> 4) + ((lane >> 2) & 1);
+                const int d = 8 * blk + 4 * ((lane >> 3) & 1) + (lane & 3);
+                const int tok = t0n + 8 * ck;
+                src = kp + (size_t)(h * D + d) * tcap + (CLAMP ? min(tok, tcap - 8) : tok);
+            } else {
+                const int vb = blk - T::KBLK;
+                const int rem = lane % T::SV;
+                const int s = 2 * (lane / T::SV) + ((rem >> 2) & 1);
+                const int j = 4 * (rem >> 3) + (rem & 3);
+                const int t = t0n + vb * T::VROWS + j;
+                src = vp + ((size_t)h * tcap + (CLAMP ? min(max(t, kst), kend - 1) : t)) * D + 8 * s;
             }
+            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + blk * T::BLK), 16, 0, 0);
         }
     }
 
@@ -371,7 +384,7 @@ struct PipeMath {
     using TM = TileMath<D, FP16, NB, NW>;
 
     f32x4 o[NB][DB], z[NB];
-    float m[NB], lm[NB];
+    float m[NB], lm[NB], thr[NB];  // running max (scaled), raw row max of the staged step, (m + TAU) / c
     f32x4 s[NB][2];      // scores of the step whose exponentials come next
     u32x4 kf[2][KS];     // K fragments of the next QK step
     u32x4 vf[DB];        // V^T fragments of the current PV step
@@ -379,7 +392,7 @@ struct PipeMath {
     __device__ void reset() {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            m[nb] = NEG_INF;
+            m[nb] = thr[nb] = NEG_INF;
             z[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int db = 0; db < DB; ++db) o[nb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -410,8 +423,10 @@ struct PipeMath {
                         if (tok < lo || tok >= hi) sn[nb][b][i] = NEG_INF;
                     }
             }
-            lm[nb] = fmaxf(fmaxf(fmaxf(sn[nb][0][0], sn[nb][0][1]), fmaxf(sn[nb][0][2], sn[nb][0][3])),
-                           fmaxf(fmaxf(sn[nb][1][0], sn[nb][1][1]), fmaxf(sn[nb][1][2], sn[nb][1][3])));
+            float mx = sn[nb][0][0];  // a chain, so that it becomes three-input maxima
+#pragma unroll
+            for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sn[nb][i >> 2][i & 3]);
+            lm[nb] = mx;
             s[nb][0] = sn[nb][0];
             s[nb][1] = sn[nb][1];
         }
@@ -419,10 +434,10 @@ struct PipeMath {
 
     // Raise the running maxima where a score of the staged step exceeds them
     // by more than TAU (wave-uniform branch, rare after the first step).
-    __device__ void rescale(float c) {
+    __device__ void rescale(float c, float rc) {  // rc = 1 / c
         bool need = false;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) need |= lm[nb] * c > m[nb] + TAU;
+        for (int nb = 0; nb < NB; ++nb) need |= lm[nb] > thr[nb];
         if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
@@ -432,6 +447,7 @@ struct PipeMath {
 #pragma unroll
                 for (int db = 0; db < DB; ++db) o[nb][db] *= alpha;
                 m[nb] = mn;
+                thr[nb] = (mn + TAU) * rc;  // raw-score threshold of the next rescale
             }
         }
     }
@@ -518,7 +534,7 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     const int nrows = p.qlen[job] * p.group;
     const int wrow0 = row0 + 16 * NB * wave;
     const bool active = wrow0 < nrows;
-    const float c = p.scale_log2;
+    const float c = p.scale_log2, rc = 1.f / p.scale_log2;
 
     u32x4 qf[NB][KS];
 #pragma unroll
@@ -566,7 +582,7 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
         TM::load_k(lds, koff, 0, acc.kf);
         TM::qk(acc.kf, qf, s0);
         acc.template finish_scores<true>(s0, kst - tb0, kend - tb0, g4);
-        acc.rescale(c);
+        acc.rescale(c, rc);
         if (nsteps > 1) TM::load_k(lds, koff, 32, acc.kf);
     }
 
@@ -592,7 +608,7 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
             const int gk = g + 2;
             acc.template block<true, false>(stage(g), 32 * (g & 1), stage(gk), 32 * (gk & 1), qf, koff, voff, 0, 32,
                                             g4, c);
-            acc.rescale(c);
+            acc.rescale(c, rc);
         }
     }
     // the last two steps: the successor of step nsteps-2 may be masked at its end
@@ -606,7 +622,7 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
             else
                 acc.template block<true, false>(stage(g), 32 * (g & 1), stage(g + 1), 32 * ((g + 1) & 1), qf, koff,
                                                 voff, 0, 32, g4, c);
-            acc.rescale(c);
+            acc.rescale(c, rc);
         }
         ++g;
     }
