@@ -144,3 +144,69 @@ def test_per_layer_attention_vs_oracle_gpu(device, monkeypatch):
         decoder.step(decoder.logits.argmax(-1).tolist())
     assert len(errors) == 4 * model.config.num_hidden_layers
     assert max(errors) <= 3e-3, errors
+
+
+def qwen3_4b_workload(seed=5):
+    """32 requests: a 2048-token prompt, a 4-way branch of 64-token nodes, 8 suffixes of 128 tokens each.
+
+    Token ids are uniform over Qwen3's 151,936-entry vocabulary.  The branch
+    nodes' length (64) is this workload's own choice; the resulting tree is
+    asserted, since random ids could merge nodes.
+    """
+    g = torch.Generator().manual_seed(seed)
+    ids = lambda n: torch.randint(0, 151_936, (n,), generator=g).tolist()  # noqa: E731
+    prompt = ids(2048)
+    sequences = []
+    for _ in range(4):
+        branch = ids(64)
+        for _ in range(8):
+            sequences.append(prompt + branch + ids(128))
+    tree = KVTree.from_sequences(sequences)
+    lengths = sorted(len(n.tokens) for n in tree.nodes if n.tokens)  # the root node is empty
+    assert lengths == [64] * 4 + [128] * 32 + [2048], "random ids merged nodes of the workload tree"
+    assert tree.storage_tokens == 2048 + 4 * 64 + 32 * 128
+    return sequences
+
+
+@pytest.mark.gpu
+def test_qwen3_4b_shaped_per_layer_attention(device, monkeypatch):
+    """Qwen3-4B-shaped random-init bf16 decoder (36 layers, hidden 2560, 32Q/8KV, d=128,
+    FFN 9728, RoPE theta 1e6): 16 greedy decode steps of the cached plan over the
+    2048 + 64 + 128 workload, every layer's attention at steps 0 and 15 against the
+    FP32 oracle on the same Q/K/V (scripts/model_checks.py:42-64)."""
+    from tree_attention import CostModel
+
+    cfg = Qwen3Config(vocab_size=151_936, hidden_size=2560, intermediate_size=9728, num_hidden_layers=36,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, rope_theta=1e6,
+                      max_position_embeddings=4096)
+    torch.manual_seed(2027)
+    previous = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(device):
+            model = Qwen3ForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(previous)
+    print("model built", flush=True)
+    sequences = qwen3_4b_workload()
+    decoder = integration.CachedPrefixDecoder(model, sequences, 16, "cube", CostModel.mi355x())
+    print("prefilled", decoder.prefix_size, "physical prompt tokens", flush=True)
+    original = integration.attention_matrix
+    errors, checking = [], {"on": False}
+
+    def checked(q, kp, vp, prepared):
+        actual = original(q, kp, vp, prepared)
+        if checking["on"]:
+            ref = request_attention(q.float().cpu(), kp.permute(2, 0, 1).float().cpu(),
+                                    vp.permute(1, 0, 2).float().cpu(), KVTree([], context_paths(decoder)))
+            errors.append(relative_l2(actual.cpu(), ref))
+        return actual
+
+    monkeypatch.setattr(integration, "attention_matrix", checked)
+    for step in range(16):
+        checking["on"] = step in (0, 15)
+        logits = decoder.step(decoder.logits.argmax(-1).tolist())
+        assert torch.isfinite(logits).all()
+        print("step", step, "max rel-L2 so far", max(errors, default=0.0), flush=True)
+    assert len(errors) == 2 * cfg.num_hidden_layers
+    assert max(errors) <= 3e-3, max(errors)
