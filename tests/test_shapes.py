@@ -55,3 +55,17 @@ def test_config_grid_is_a_full_factorial():
             (2 ** i) * (shared // params["depth"] + (1 if i < shared % params["depth"] else 0))
             for i in range(params["depth"])) + params["requests"] * (params["context"] - shared)
         assert leaves <= params["requests"]
+
+
+def test_grid_comparisons_geometric_mean():
+    """benchmark_grid.comparisons follows scripts/analyze_planning.py:60-64."""
+    from tree_attention.benchmark_grid import comparisons
+    rows = []
+    for i, (req, cube) in enumerate([(4.0, 1.0), (9.0, 1.0), (2.0, 4.0)]):
+        for method, t in (("request", req), ("fixed", 2.0), ("greedy", 1.0), ("cube", cube)):
+            rows.append({"shape": {"i": i}, "method": method, "kernel_us": t, "refresh_us": 2 * t})
+    c = comparisons(rows)
+    r = c["kernel_us_vs_request"]
+    assert abs(r["geometric_mean_speedup"] - (4 * 9 * 0.5) ** (1 / 3)) < 1e-12
+    assert r["median_speedup"] == 4.0 and r["range"] == [0.5, 9.0] and r["faster_shapes"] == 2
+    assert c["refresh_us_vs_greedy"]["shapes"] == 3
