@@ -21,10 +21,11 @@ each kernel's share of a graph of back-to-back launches, gaps included.  The
 roofline figure divides the dominant kernel's algorithmic work by its
 ``kernel_us``.
 
-The CPU leg times the FP32 oracle (oracle/attention_oracle.py, the restatement
-of the reference's reference.py) on the host cores on the same layer, and is
-also the parity gate: the GPU output must be within 0.3% relative L2 of the
-oracle's per-request attention.
+The parity gate comes first: the GPU output must be within 0.3% relative L2
+of the FP32 oracle's per-request attention (oracle/attention_oracle.py, the
+restatement of the reference's reference.py).  The CPU leg times the oracle
+on the host cores on the same layer after the GPU timing, so that the GPU
+does not idle (and drop its clocks) right before the timed steps.
 
 Prints one JSON line (see the repository's bench contract).
 """
@@ -55,7 +56,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--method", default="cube")
     ap.add_argument("--cost-model", default="mi355x", choices=["mi355x", "reference"])
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
@@ -114,8 +115,8 @@ def main():
         print(json.dumps({"error": "pools with equal contents gave different outputs"}), flush=True)
         sys.exit(1)
 
-    # CPU leg first: the oracle on the host is also the parity gate before any timing
-    cpu, rel = cpu_baseline(q, k, v, tree, plan, eager[0].cpu(), args.cpu_budget_s)
+    # parity gate before any timing: the GPU layer against the oracle's per-request attention
+    rel = parity_rel_l2(q, k, v, tree, eager[0].cpu())
     if not rel <= REL_L2_BOUND:
         print(json.dumps({"error": "parity gate failed", "rel_l2": rel}), flush=True)
         sys.exit(1)
@@ -201,6 +202,9 @@ def main():
     per_request_us = time_steps(lambda i: attention_matrix(qd, *pools[i % POOLS], req_prepared),
                                 max(POOLS, args.steps // 4), max(2, args.warmup // 2))
 
+    # CPU leg after the GPU timing (the GPU would idle through it and start the timing cold)
+    cpu = cpu_baseline(q, k, v, tree, plan, args.cpu_budget_s)
+
     # ---- roofline of the dominant kernel
     jobs = prepared.jobs
     small_rows = HQ // HK
@@ -208,8 +212,10 @@ def main():
     tail_jobs = sorted({j for j, _, _ in prepared.items[_native.TA_TAIL].view(-1, 3).tolist()})
     tail_requests = [jobs[j].requests[0] for j in tail_jobs]
     counts = prepared.counts.tolist()
-    large_flops = sum(4 * len(j.requests) * HQ * len(j.tokens) * D for j in jobs
-                      if len(j.requests) * small_rows > 16)
+    # the large kernels' work: their jobs, plus the private segments attached to their items
+    large_flops = (sum(4 * len(j.requests) * HQ * len(j.tokens) * D for j in jobs
+                       if len(j.requests) * small_rows > 16)
+                   + sum(4 * HQ * len(t.tokens) * D for segs in prepared.attached.values() for t, _ in segs))
     dominant = max(kernel_us, key=kernel_us.get)
     traffic = _pmc_traffic(dominant)
     if dominant.startswith("segment_large"):
@@ -217,7 +223,8 @@ def main():
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1),
                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
-                    "algorithmic": f"{large_flops} FLOP per launch (4 x rows x tokens x D over the large jobs)"}
+                    "algorithmic": f"{large_flops} FLOP per launch (4 x rows x tokens x D over the large jobs "
+                                   f"and their attached private segments)"}
     else:
         if dominant == "segment_small":
             nbytes = physical_kv_bytes(small_tokens)
@@ -274,16 +281,20 @@ def _pmc_traffic(kernel_name):
         return None
 
 
-def cpu_baseline(q, k, v, tree, plan, gpu_out, budget_s):
-    """CPU leg: the FP32 oracle on the host cores (timed), and the parity check of ``gpu_out``.
-
-    Times the oracle's plan-driven ``segmented_attention`` (reference.py:16-33)
-    on the same layer and plan (median of up to 5 runs within ``budget_s``),
-    and returns the relative L2 of the GPU output against the oracle's
-    ``request_attention`` (reference.py:4-13).
-    """
+def parity_rel_l2(q, k, v, tree, gpu_out):
+    """Relative L2 of ``gpu_out`` against the oracle's FP32 ``request_attention`` (reference.py:4-13)."""
     import torch
-    from oracle.attention_oracle import relative_l2, request_attention, segmented_attention
+    from oracle.attention_oracle import relative_l2, request_attention
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    return relative_l2(gpu_out, request_attention(q.float(), k.float(), v.float(), tree))
+
+
+def cpu_baseline(q, k, v, tree, plan, budget_s):
+    """CPU leg: the FP32 oracle's plan-driven ``segmented_attention``
+    (reference.py:16-33) on the host cores, on the same layer and plan
+    (median of up to 5 runs within ``budget_s``)."""
+    import torch
+    from oracle.attention_oracle import segmented_attention
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     qf, kf, vf = q.float(), k.float(), v.float()
@@ -297,13 +308,11 @@ def cpu_baseline(q, k, v, tree, plan, gpu_out, budget_s):
             break
     us = statistics.median(times) * 1e6
     gbs = physical_kv_bytes(tree.storage_tokens) / (us * 1e-6) / 1e9
-    rel = relative_l2(gpu_out, request_attention(qf, kf, vf, tree))
-    cpu = {"value": round(gbs, 3), "unit": "GB/s", "us_per_layer": round(us, 1), "cores": cores,
+    return {"value": round(gbs, 3), "unit": "GB/s", "us_per_layer": round(us, 1), "cores": cores,
            "threads": torch.get_num_threads(), "kind": "port",
            "sample": f"{len(times)} full layer(s) of the same workload and plan through the oracle's "
                      f"segmented_attention in fp32 (median)",
            "cpu": platform.processor() or platform.machine()}
-    return cpu, rel
 
 
 if __name__ == "__main__":

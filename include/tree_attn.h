@@ -72,12 +72,23 @@ typedef struct ta_plan {
     const int32_t *items[TA_NKINDS];  /* work-item triples per kind TA_SMALL .. TA_TAIL */
     int32_t n_items[TA_NKINDS];       /* number of triples per kind                 */
     const int32_t *rest;      /* [n_rest] requests without a TA_TAIL job: the ones
-                                 the merge kernel of ta_attention_matrix covers    */
+                                 the merge kernel of ta_attention_matrix covers;
+                                 NULL with n_rest == nreq: every request         */
     void *part;               /* [nslot, hq, d] fp16, row-scaled                   */
     float *lse;               /* [nslot, hq, 2]                                    */
     int32_t njobs, maxr, maxs, nreq, nslot;
     int32_t hq, hk, d, dtype;
     int32_t n_rest;
+    /* Attached private segments of the TA_LARGE256 items (NULL: none), an
+     * execution detail with no counterpart in the reference: xtail_stride ints
+     * per TA_LARGE256 item -- the number of segments n, then (first physical
+     * token, tokens, first job row) for each of the n.  The segment's tokens
+     * belong to the request whose group query rows start at that job row
+     * (rows of one wave, 32 rows); the item folds them into that request's
+     * partial rows, so the segment has no partial slot of its own.  Needs
+     * tcap % 8 == 0 (ta_attention_matrix returns TA_ERR_ARG otherwise). */
+    const int32_t *xtail;
+    int32_t xtail_stride;
 } ta_plan;
 
 /* Version string of the library build. */
@@ -120,6 +131,15 @@ int ta_attention_matrix(const void *q, const void *kp, const void *vp,
  * (kernels.py:58-83).  Needs tcap % 8 == 0 (TA_ERR_ARG otherwise). */
 int ta_tail_merge(const void *q, const void *kp, const void *vp,
                   int32_t tcap, const ta_plan *plan, void *out, void *stream);
+
+/* One segment launch of a prepared plan: the work items of `kind`, writing
+ * partials (TA_TAIL items included), with the plan's attached segments for
+ * TA_LARGE256.  Counterpart of the reference's direct _segment launches in
+ * scripts/calibrate_tiles.py:24-29 and scripts/profile_kernel.py:17-20, which
+ * pass the prepared plan's tensors; TA_ERR_ARG for a plan with attached
+ * segments on pools with tcap % 8 != 0. */
+int ta_segment_plan(const void *q, const void *kp, const void *vp, int32_t tcap,
+                    const ta_plan *plan, int32_t kind, void *stream);
 
 /* Kernel timing hook.  No counterpart in the reference, which times kernels
  * with device events around whole launches (scripts/profile_kernel.py:17-33).

@@ -216,6 +216,40 @@ def test_attention_packs_and_c_abi_phases_agree(name, device):
     assert relative_l2(b.cpu(), c.cpu().float()) < 5e-4
 
 
+@pytest.mark.parametrize("hq,hk,d,dtype,pad", [(32, 8, 128, torch.bfloat16, 0), (32, 4, 64, torch.float16, 8),
+                                                (32, 2, 32, torch.bfloat16, 0), (32, 8, 128, torch.bfloat16, 3)])
+def test_attached_tails(hq, hk, d, dtype, pad, device):
+    """Private tails folded into 256-row root items: ragged lengths (1..200 tokens, unaligned
+    starts, several tiles), several per item, GQA groups 4/8/16; equal to the oracle, to the
+    unattached plan, and to the explicit segment + merge launches.  pad 3 (pool capacity not a
+    multiple of 8) runs the unattached variant on the register-staged kernels."""
+    group = hq // hk
+    nreq, root = {4: (96, 3001), 8: (48, 6001), 16: (24, 12001)}[group]
+    tails = [1 + (37 * r) % 200 for r in range(nreq)]
+    tree = shapes.tree(shapes.shared_prefix(nreq, root, tails))
+    q, k, v = make_inputs(tree, hq, hk, d, dtype, 31 + group, tcap=tree.storage_tokens + pad)
+    ref = oracle_fp32(q, k, v, tree)
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    plan = schedule(tree, hq, hk, d, "cube", MI355X_LIKE)
+    p1 = prepare(plan, qd)
+    assert p1.attached, "the shape must attach tails"
+    assert any(len(job.tokens) > 64 for segs in p1.attached.values() for job, _ in segs)
+    assert group != 4 or max(len(v) for v in p1.attached.values()) >= 2
+    say("attached", hq, hk, d, dtype, pad, len(p1.attached), p1.small_jobs)
+    a = attention_matrix(qd, kp, vp, p1).clone()
+    p2 = prepare(plan, qd, attach_tails=False)
+    b = attention_matrix(qd, kp, vp, p2).clone()
+    p1.out.zero_()
+    for kind in range(_native.TA_NKINDS):
+        segment(qd, kp, vp, p1, kind)
+    c = merge(p1, kp).clone()
+    torch.cuda.synchronize()
+    check(a, ref, 0.008, 0.03, "attached")
+    check(b, ref, 0.008, 0.03, "unattached")
+    check(c, ref, 0.008, 0.03, "attached/segment+merge")
+
+
 @pytest.mark.parametrize("vscale", [1e5, 1e-5])
 def test_partial_rows_keep_range(vscale, device):
     """Partial rows are fp16 scaled by 2^-e per row: V far outside fp16's range
@@ -333,7 +367,15 @@ def test_full_size_properties(device):
     kp3, vp3 = pack_kv(k2[idx].to(device), v[idx].to(device))
     b = attention_matrix(q[perm].contiguous().to(device), kp3, vp3, prepared).clone()
     torch.cuda.synchronize()
-    assert relative_l2(b.cpu(), a[perm.to(device)].cpu()) < 1e-6
+    # each private tail is attended inside the root chunk item its request index selects, so a
+    # permuted request's tail joins another chunk's fp16 partial: equal up to partial rounding
+    # (an indexing mistake gives O(1) differences)
+    assert relative_l2(b.cpu(), a[perm.to(device)].cpu()) < 2e-3
+    plain = prepare(schedule(tree, 32, 8, 128, "cube", MI355X_LIKE), qd, attach_tails=False)
+    a = attention_matrix(qd, kp2, vp, plain).clone()
+    b = attention_matrix(q[perm].contiguous().to(device), kp3, vp3, plain).clone()
+    torch.cuda.synchronize()
+    assert relative_l2(b.cpu(), a[perm.to(device)].cpu()) < 1e-6  # symmetric work split: exact
 
 
 def test_bad_inputs_raise(device):

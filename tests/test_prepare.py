@@ -9,11 +9,14 @@ from tree_attention.schedule import Job, Plan
 
 
 def _covers_paths(prepared, tree):
-    """Every request's execution jobs cover its path exactly once."""
+    """Every request's execution jobs and attached segments cover its path exactly once."""
     seen = [[] for _ in tree.paths]
     for job in prepared.jobs:
         for r in job.requests:
             seen[r].extend(job.tokens)
+    for segs in prepared.attached.values():
+        for job, _ in segs:
+            seen[job.requests[0]].extend(job.tokens)
     return all(sorted(seen[r]) == sorted(path) for r, path in enumerate(tree.paths))
 
 
@@ -140,3 +143,71 @@ def test_tail_items_and_merge_rest():
     # request 1 has two small jobs, 2 and 3 share one, 4 and 5 have only the large job
     assert p.rest.tolist() == [1, 2, 3, 4, 5] and p.abi.n_rest == 5
     assert p.abi.n_items[_native.TA_SMALL] == 3 * 2
+
+
+def test_private_tails_attach_to_root_items():
+    """Headline under the MI355X model: each private tail is folded into one 256-row
+    root work item holding its request's rows (four per item, on four waves)."""
+    tree = shapes.tree(shapes.headline())
+    q = torch.empty(128, 32, 128, dtype=torch.bfloat16)
+    p = prepare(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q)
+    assert p.small_jobs == 0 and len(p.jobs) == 16
+    assert _covers_paths(p, tree)
+    assert p.abi.n_items[_native.TA_TAIL] == 0 and p.abi.n_items[_native.TA_SMALL] == 0
+    assert p.counts.tolist() == [16] * 128 and p.abi.n_rest == 128
+    assert sorted(len(v) for v in p.attached.values()) == [4] * 32
+    tails = sorted(job.requests[0] for segs in p.attached.values() for job, _ in segs)
+    assert tails == list(range(128))
+    for (j, row0), segs in p.attached.items():
+        job = p.jobs[j]
+        waves = set()
+        for tail, lrow in segs:
+            r = tail.requests[0]
+            assert lrow == job.requests.index(r) * 4 and row0 <= lrow < row0 + 256
+            waves.add((lrow - row0) // 32)
+        assert len(waves) == len(segs)  # one tail per wave of the item
+    # device record: per TA_LARGE256 item (job, row0, head) the same segments
+    stride = p.abi.xtail_stride
+    xt = p.xtail.view(-1, stride).tolist()
+    items = p.items[_native.TA_LARGE256].view(-1, 3).tolist()
+    assert len(xt) == len(items) == 256
+    for rec, (j, row0, h) in zip(xt, items):
+        segs = p.attached[(j, row0)]
+        assert rec[0] == len(segs)
+        assert rec[1:1 + 3 * len(segs)] == [v for tail, lrow in segs for v in (tail.tokens[0], len(tail.tokens), lrow)]
+    # without attachment the tails are TA_TAIL jobs again
+    p2 = prepare(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q, attach_tails=False)
+    assert not p2.attached and p2.xtail is None and p2.abi.xtail is None
+    assert p2.abi.n_items[_native.TA_TAIL] == 128 * 8 and _covers_paths(p2, tree)
+
+
+def test_attachment_limits():
+    """Tails attach only where the request's rows fit one wave, only up to the item's own
+    tile count, and never for growing decode tails."""
+    settings = dict(kvheads=1)
+    q = torch.empty(80, 4, 32, dtype=torch.float16)   # group 4: 80 requests = 320 rows
+    root = Job(tuple(range(80)), tuple(range(0, 64)))  # one tile of root tokens
+    tails = [Job((r,), tuple(range(64 + 16 * r, 80 + 16 * r))) for r in range(80)]
+    p = prepare(Plan([root] + tails, "x", 0.0, settings), q)
+    # two row tiles (rows 0-255, 256-319) of one job, each may take one tile of tails
+    assert sorted((j, row0, len(s)) for (j, row0), s in p.attached.items()) == [(p.small_jobs, 0, 1),
+                                                                                  (p.small_jobs, 256, 1)]
+    assert len(p.jobs) == p.small_jobs + 1
+    tree_paths = [tuple(range(0, 64)) + tuple(range(64 + 16 * r, 80 + 16 * r)) for r in range(80)]
+    seen = [[] for _ in range(80)]
+    for job in p.jobs:
+        for r in job.requests:
+            seen[r].extend(job.tokens)
+    for segs in p.attached.values():
+        for job, _ in segs:
+            seen[job.requests[0]].extend(job.tokens)
+    assert all(sorted(seen[r]) == list(tree_paths[r]) for r in range(80))
+    # growing tails (fixed_from) stay jobs of their own
+    p = prepare(Plan([root] + tails, "x", 0.0, settings), q, fixed_from=64)
+    assert not p.attached
+    # group 12: request 1's rows 12-23 lie in wave 0; request 2's rows 24-35 straddle waves 0 and 1
+    q = torch.empty(24, 12, 32, dtype=torch.float16)
+    root = Job(tuple(range(24)), tuple(range(0, 256)))
+    p = prepare(Plan([root, Job((1,), (300, 301)), Job((2,), (302, 303))], "x", 0.0, settings), q)
+    assert [(job.requests, lrow) for segs in p.attached.values() for job, lrow in segs] == [((1,), 12)]
+    assert [job.requests for job in p.jobs[:p.small_jobs]] == [(2,)]

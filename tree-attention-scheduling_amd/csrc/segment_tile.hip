@@ -48,6 +48,19 @@ typedef __attribute__((address_space(3))) void lds_void;
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
 #define TA_VMCNT(n) ((((n)&15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
 
+// Wait until at most n tiles of this wave's copies (BPW each) are in flight
+// (n = 0 .. 3; the immediate of s_waitcnt must be a constant).
+template <int BPW>
+__device__ inline void wait_tiles(int n) {
+    static_assert(3 * BPW <= 63, "three tiles of copies fit the vmcnt counter");
+    switch (n) {
+        case 3: __builtin_amdgcn_s_waitcnt(TA_VMCNT(3 * BPW)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(TA_VMCNT(2 * BPW)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(TA_VMCNT(BPW)); break;
+        default: __builtin_amdgcn_s_waitcnt(TA_VMCNT(0)); break;
+    }
+}
+
 // Two transposing LDS loads -> one 8-element MFMA operand.
 __device__ inline u32x4 tr_pair(const u16 *lo, const u16 *hi) {
     const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)lo);
@@ -57,21 +70,60 @@ __device__ inline u32x4 tr_pair(const u16 *lo, const u16 *hi) {
 }
 
 // LDS layout of one 64-token tile (16-bit elements): KBLK blocks of K, then
-// VBLK blocks of V, each a 1 KiB copy unit padded to BLK elements.
+// VBLK blocks of V, each a 1 KiB copy unit of 64 16-byte slots.
 //   K block b: d-rows 8b..8b+7; the 16-byte chunk c (tokens 8c..8c+7) of
-//     d-row 8b+j sits in slot 16*(c>>1) + 8*(j>>2) + 4*(c&1) + (j&3).
+//     d-row 8b+j has logical slot 16*(c>>1) + 8*(j>>2) + 4*(c&1) + (j&3).
 //   V block b: token rows VROWS*b ..; chunk s (d = 8s..8s+7) of token row j
-//     sits in slot SV*(s>>1) + 8*(j>>2) + 4*(s&1) + (j&3).
+//     has logical slot SV*(s>>1) + 8*(j>>2) + 4*(s&1) + (j&3).
+// Swizzle: in odd blocks (block index within the tile) logical slot l sits at
+// physical slot l ^ 8, i.e. the two 128-byte halves of every 256 bytes are
+// swapped.  The four 16-lane groups of a transposing read address blocks of
+// alternating parity at equal logical offsets, so the groups land 128 bytes
+// apart modulo 256 (disjoint LDS banks) without padding the blocks; a tile is
+// 32 KiB and five of them fit the 160 KiB LDS.
+struct LdsOfs {  // per-lane element offsets of the transposing reads (swizzle applied)
+    int klo, khi;        // K: the two 8-byte halves of a lane's operand
+    int vlo[2], vhi[2];  // V: same, by the parity of the 16-row block db of O^T
+};
+
 template <int D>
 struct Tile {
     static constexpr int TT = 64;
-    static constexpr int BLK = 576;         // 1 KiB block + 128 B padding
+    static constexpr int BLK = 512;         // 1 KiB block
     static constexpr int KBLK = D / 8;
     static constexpr int VROWS = 512 / D;   // token rows per V block
     static constexpr int VBLK = TT / VROWS;
     static constexpr int NBLK = KBLK + VBLK;
     static constexpr int ELEMS = NBLK * BLK;
     static constexpr int SV = 1024 / D;
+
+    // physical element offset of logical in-block offset `e` in block `b`
+    __device__ static int swz(int b, int e) { return e ^ (64 * (b & 1)); }
+
+    // Lane (row, g4) of a transposing read addresses, within its block,
+    // logical element 8 * (4 * ((row & 3) >> 1) + (row >> 2)) + 4 * (row & 1)
+    // (< 64) of the chunk-slot group it reads; the K operand's two halves are
+    // 64 elements apart in block 4 ks + g4 (a parity of g4 & 1 for every ks);
+    // the V operand's halves are in blocks KBLK + base / VROWS + vb and
+    // 16 / VROWS blocks further (base / VROWS is even), at in-block offset
+    // 8 SV db + vin, whose bit 6 depends on db only through SV / 8 (odd for
+    // D = 128).
+    __device__ static LdsOfs offsets(int row, int g4) {
+        const int lane_ofs = 8 * (4 * ((row & 3) >> 1) + (row >> 2)) + 4 * (row & 1);
+        LdsOfs o;
+        o.klo = BLK * g4 + swz(g4, lane_ofs);
+        o.khi = BLK * g4 + swz(g4, lane_ofs + 64);
+        const int vb = (4 * g4) / VROWS;
+        const int vin = 64 * (((4 * g4) % VROWS) >> 2) + lane_ofs;
+        const int blo = KBLK + vb, bhi = blo + 16 / VROWS;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int dbo = 8 * SV * e;  // representative db of parity e
+            o.vlo[e] = BLK * vb + swz(blo, dbo + vin) - dbo;
+            o.vhi[e] = BLK * (vb + 16 / VROWS) + swz(bhi, dbo + vin) - dbo;
+        }
+        return o;
+    }
 };
 
 template <int D, bool FP16, int NB, int NW>
@@ -100,10 +152,10 @@ struct TileMath {
     // compiler keep the copies in flight across the reads of `cur`.
     __device__ void step(const u16 *__restrict__ cur, u16 *__restrict__ nxt, bool copy, bool compute,
                          const u16 *__restrict__ kp, const u16 *__restrict__ vp, int h, int tcap, int t0n, int kst,
-                         int kend, int wave, int lane, const u32x4 (&qf)[NB][KS], int koff, int voff, int lo,
+                         int kend, int wave, int lane, const u32x4 (&qf)[NB][KS], const LdsOfs &of, int lo,
                          int hi, int g4, float c) {
         if (copy) this->copy(nxt, kp, vp, h, tcap, t0n, kst, kend, wave, lane);
-        if (compute) tile(cur, qf, koff, voff, lo, hi, g4, c);
+        if (compute) tile(cur, qf, of, lo, hi, g4, c);
     }
 
     // Copy the tile at pool token t0n into stage `st` (this wave's blocks).
@@ -129,15 +181,16 @@ struct TileMath {
             // with KBLK % NW == 0 every wave's i-th block is K for the same i
             const bool isk = T::KBLK % NW == 0 ? i * NW < T::KBLK : blk < T::KBLK;
             const u16 *src;
+            const int l = lane ^ (8 * (blk & 1));  // logical slot filled by this lane (swizzle)
             if (isk) {
-                const int ck = 2 * (lane >> 4) + ((lane >> 2) & 1);
-                const int d = 8 * blk + 4 * ((lane >> 3) & 1) + (lane & 3);
+                const int ck = 2 * (l >> 4) + ((l >> 2) & 1);
+                const int d = 8 * blk + 4 * ((l >> 3) & 1) + (l & 3);
                 const int tok = t0n + 8 * ck;
                 src = kp + (size_t)(h * D + d) * tcap + (CLAMP ? min(tok, tcap - 8) : tok);
             } else {
                 const int vb = blk - T::KBLK;
-                const int rem = lane % T::SV;
-                const int s = 2 * (lane / T::SV) + ((rem >> 2) & 1);
+                const int rem = l % T::SV;
+                const int s = 2 * (l / T::SV) + ((rem >> 2) & 1);
                 const int j = 4 * (rem >> 3) + (rem & 3);
                 const int t = t0n + vb * T::VROWS + j;
                 src = vp + ((size_t)h * tcap + (CLAMP ? min(max(t, kst), kend - 1) : t)) * D + 8 * s;
@@ -148,15 +201,27 @@ struct TileMath {
 
     // K fragments (A operand of QK) of the 32 tokens base .. base+31:
     // kf[b][ks] covers tokens base+16b .. +15, d = 32*ks .. +31.
-    __device__ static void load_k(const u16 *__restrict__ cur, int koff, int base, u32x4 (&kf)[2][KS]) {
+    __device__ static void load_k(const u16 *__restrict__ cur, const LdsOfs &of, int base, u32x4 (&kf)[2][KS]) {
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 // block 4*ks + g4, chunk pair base/16 + b, block rows 0-3 / 4-7
-                const u16 *ka = cur + koff + 4 * T::BLK * ks + 8 * (base + 16 * b);
-                kf[b][ks] = tr_pair(ka, ka + 64);
+                const int e = 4 * T::BLK * ks + 8 * (base + 16 * b);
+                kf[b][ks] = tr_pair(cur + of.klo + e, cur + of.khi + e);
             }
+    }
+
+    // V^T fragments (A operand of PV) of the 32 tokens base .. base+31: PV
+    // k-slot j of lane group g4 is token 4*g4+j (j<4) or 16+4*g4+j-4 (j>=4),
+    // where the QK output left P.
+    __device__ static void load_v(const u16 *__restrict__ st, const LdsOfs &of, int base, u32x4 (&v)[DB]) {
+        const u16 *vrow = st + T::BLK * (T::KBLK + base / T::VROWS);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const u16 *va = vrow + 8 * T::SV * db;
+            v[db] = tr_pair(va + of.vlo[db & 1], va + of.vhi[db & 1]);
+        }
     }
 
     // S^T = K Q^T: s[nb][b] holds tokens base+16b+4*g4+i of row block nb.
@@ -171,37 +236,30 @@ struct TileMath {
                 for (int nb = 0; nb < NB; ++nb) s[nb][b] = O::mma_k32(kf[b][ks], qf[nb][ks], s[nb][b]);
     }
 
-    // koff / voff: per-lane element offsets of the transposing loads;
+    // of: per-lane element offsets of the transposing loads;
     // tokens [lo, hi) of the tile belong to the job.  Software pipeline per
     // 32-token step k: the LDS loads of step k's V and step k+1's K are issued
     // before step k's softmax (which hides their latency), then PV of step k
     // and QK of step k+1 run back to back on the matrix cores.
-    __device__ void tile(const u16 *__restrict__ cur, const u32x4 (&qf)[NB][KS], int koff, int voff, int lo,
+    __device__ void tile(const u16 *__restrict__ cur, const u32x4 (&qf)[NB][KS], const LdsOfs &of, int lo,
                          int hi, int g4, float c) {
         constexpr int STEPS = T::TT / 32;
         const u32x4 ones = {O::ONE2, O::ONE2, O::ONE2, O::ONE2};
         f32x4 s[NB][2];
         {
             u32x4 kf[2][KS];
-            load_k(cur, koff, 0, kf);
+            load_k(cur, of, 0, kf);
             qk(kf, qf, s);
         }
 #pragma unroll
         for (int k = 0; k < STEPS; ++k) {
             const int base = 32 * k;
             if (base >= hi) break;
-            // V^T fragments of this step: PV k-slot j of lane group g4 is token
-            // 4*g4+j (j<4) or 16+4*g4+j-4 (j>=4), where the QK output left P.
             u32x4 vf[DB];
-            const u16 *vrow = cur + voff + T::BLK * (T::KBLK + base / T::VROWS);
-#pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const u16 *va = vrow + 8 * T::SV * db;
-                vf[db] = tr_pair(va, va + T::BLK * (16 / T::VROWS));
-            }
+            load_v(cur, of, base, vf);
             const bool more = k + 1 < STEPS && base + 32 < hi;
             u32x4 kf[2][KS];
-            if (more) load_k(cur, koff, base + 32, kf);
+            if (more) load_k(cur, of, base + 32, kf);
             if (lo > base || hi < base + 32) {  // wave-uniform: first or last step of the job
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
@@ -304,11 +362,7 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
 
     M acc;
     acc.reset();
-    // Lane part of the transposing-load offsets: block (K) or token group (V)
-    // g4, slot 4*((row&3)>>1) + (row>>2), 8-byte half row&1.
-    const int lane_ofs = 8 * (4 * ((row & 3) >> 1) + (row >> 2)) + 4 * (row & 1);
-    const int koff = T::BLK * g4 + lane_ofs;
-    const int voff = T::BLK * ((4 * g4) / T::VROWS) + 64 * (((4 * g4) % T::VROWS) >> 2) + lane_ofs;
+    const LdsOfs of = T::offsets(row, g4);
 
     const int tb0 = kst & ~7;
     const int ntiles = ntok > 0 ? (kend - tb0 + T::TT - 1) / T::TT : 0;
@@ -320,7 +374,7 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
             acc.copy(lds, p.kp, p.vp, h, p.tcap, t0, kst, kend, wave, lane);
             __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
             __builtin_amdgcn_s_barrier();
-            if (active) acc.tile(lds, qf, koff, voff, max(0, kst - t0), min(T::TT, kend - t0), g4, p.scale_log2);
+            if (active) acc.tile(lds, qf, of, max(0, kst - t0), min(T::TT, kend - t0), g4, p.scale_log2);
         }
     } else {
     // Iteration it copies tile it+STAGES-1 and computes tile it (stage it %
@@ -341,7 +395,7 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
         const int ns = cs == 0 ? STAGES - 1 : cs - 1;  // stage of tile it+AHEAD (that of tile it-1)
         const int t0 = tb0 + it * T::TT;
         acc.step(lds + cs * T::ELEMS, lds + ns * T::ELEMS, it + AHEAD < ntiles, it >= 0 && active, p.kp, p.vp, h,
-                 p.tcap, t0 + AHEAD * T::TT, kst, kend, wave, lane, qf, koff, voff, max(0, kst - t0),
+                 p.tcap, t0 + AHEAD * T::TT, kst, kend, wave, lane, qf, of, max(0, kst - t0),
                  min(T::TT, kend - t0), g4, p.scale_log2);
         cs = cs == STAGES - 1 ? 0 : cs + 1;
     }
@@ -372,7 +426,7 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
 // and the rare online-softmax rescale runs between blocks.  The order inside
 // a block is pinned with sched_group_barrier so that MFMAs and VALU
 // instructions alternate in each wave's instruction stream.  K/V tiles arrive
-// by LDS DMA into four stages: tiles t and t+1 are read while t+2 and t+3 are
+// by LDS DMA into five stages: tiles t and t+1 are read while t+2 .. t+4 are
 // in flight, with one barrier per tile.
 template <int D, bool FP16, int NW>
 struct PipeMath {
@@ -396,15 +450,6 @@ struct PipeMath {
             z[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int db = 0; db < DB; ++db) o[nb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-
-    __device__ static void load_v(const u16 *__restrict__ st, int voff, int base, u32x4 (&v)[DB]) {
-        const u16 *vrow = st + voff + T::BLK * (T::KBLK + base / T::VROWS);
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            const u16 *va = vrow + 8 * T::SV * db;
-            v[db] = tr_pair(va, va + T::BLK * (16 / T::VROWS));
         }
     }
 
@@ -456,14 +501,14 @@ struct PipeMath {
     // ks / kbase: of K(g+2) (any resident step when there is none); lo / hi:
     // valid tokens of step g+1.  Every fragment register set is reloaded only
     // after its last reader: V(g) during QK(g+1), K(g+2) during PV(g).
-    template <bool MORE, bool MASKN>
+    template <bool MORE, bool MASKN, bool ROWMASK = false>
     __device__ __forceinline__ void block(const u16 *__restrict__ vs, int vbase, const u16 *__restrict__ ks,
-                                          int kbase, const u32x4 (&qf)[NB][KS], int koff, int voff, int lo,
-                                          int hi, int g4, float c) {
+                                          int kbase, const u32x4 (&qf)[NB][KS], const LdsOfs &of, int lo,
+                                          int hi, int g4, float c, unsigned keep = ~0u) {
         const u32x4 ones = {O::ONE2, O::ONE2, O::ONE2, O::ONE2};
         f32x4 sn[NB][2];
         if (MORE) TM::qk(kf, qf, sn);
-        load_v(vs, voff, vbase, vf);
+        TM::load_v(vs, of, vbase, vf);
         u32x4 pb[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -472,6 +517,7 @@ struct PipeMath {
             for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(__builtin_fmaf(s[nb][i >> 2][i & 3], c, -m[nb]));
             pb[nb] = u32x4{O::pack(pr[0], pr[1]), O::pack(pr[2], pr[3]), O::pack(pr[4], pr[5]),
                            O::pack(pr[6], pr[7])};
+            if (ROWMASK && !((keep >> nb) & 1)) pb[nb] = u32x4{0u, 0u, 0u, 0u};
         }
         if (MORE) {
             // 2*KS*NB QK MFMAs; the V reads go out with the first half of them
@@ -491,7 +537,7 @@ struct PipeMath {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) z[nb] = O::mma_k32(ones, pb[nb], z[nb]);
         if (MORE) {
-            TM::load_k(ks, koff, kbase, kf);
+            TM::load_k(ks, of, kbase, kf);
             finish_scores<MASKN>(sn, lo, hi, g4);
         }
         // instruction order: QK MFMAs alternate with the exponentials and the
@@ -506,18 +552,46 @@ struct PipeMath {
             }
         }
     }
+
+    // One staged tile of an attached private segment (after the pipeline has
+    // drained): tokens [lo, hi) of the tile, for this wave's rows [rlo, rhi)
+    // only.  Other rows get P = 0 and keep their running maxima, so their
+    // state is unchanged.
+    __device__ void tail_tile(const u16 *__restrict__ st, const u32x4 (&qf)[NB][KS], const LdsOfs &of, int lo,
+                              int hi, int rlo, int rhi, int row, int g4, float c, float rc) {
+        unsigned keep = 0;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) keep |= (unsigned)(16 * nb + row >= rlo && 16 * nb + row < rhi) << nb;
+#pragma unroll
+        for (int k = 0; k < T::TT / 32; ++k) {
+            const int base = 32 * k;
+            if (base >= hi) break;
+            f32x4 sn[NB][2];
+            TM::load_k(st, of, base, kf);
+            TM::qk(kf, qf, sn);
+            finish_scores<true>(sn, lo - base, hi - base, g4);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                if (!((keep >> nb) & 1)) lm[nb] = NEG_INF;
+            rescale(c, rc);
+            block<false, false, true>(st, base, st, 0, qf, of, 0, 32, g4, c, keep);
+        }
+    }
 };
 
-template <int D, bool FP16, int NW>
+#ifndef TA_PIPE_STAGES
+#define TA_PIPE_STAGES 5
+#endif
+
+template <int D, bool FP16, int NW, int STAGES = TA_PIPE_STAGES>
 __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     using T = Tile<D>;
     using M = PipeMath<D, FP16, NW>;
     using TM = TileMath<D, FP16, 2, NW>;
     constexpr int NB = M::NB, KS = M::KS;
-    constexpr int STAGES = 4;
     constexpr int BPW = T::NBLK / NW;  // copies per wave per tile
     static_assert(T::NBLK % NW == 0, "every wave copies the same number of blocks");
-    static_assert(2 * BPW <= 63, "two tiles of copies fit the vmcnt counter");
+    static_assert(STAGES >= 4 && STAGES <= 5, "the pipelined steps read two tiles; up to three more in flight");
     __shared__ __attribute__((aligned(16))) u16 lds[STAGES * T::ELEMS];
 
     const int total = gridDim.x;
@@ -535,70 +609,106 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     const int wrow0 = row0 + 16 * NB * wave;
     const bool active = wrow0 < nrows;
     const float c = p.scale_log2, rc = 1.f / p.scale_log2;
-
-    u32x4 qf[NB][KS];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        const int rr = wrow0 + 16 * nb + row;
-        if (rr < nrows) {
-            const int lr = rr / p.group, gg = rr - lr * p.group;
-            const int rq = p.qids[(size_t)job * p.maxr + lr];
-            const u16 *src = p.q + ((size_t)rq * p.hq + h * p.group + gg) * D + 8 * g4;
-#pragma unroll
-            for (int k = 0; k < KS; ++k) qf[nb][k] = *(const u32x4 *)(src + 32 * k);
-        } else {
-#pragma unroll
-            for (int k = 0; k < KS; ++k) qf[nb][k] = u32x4{0, 0, 0, 0};
-        }
-    }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int k = 0; k < KS; ++k) asm volatile("" : "+v"(qf[nb][k]));
-
-    M acc;
-    acc.reset();
-    const int lane_ofs = 8 * (4 * ((row & 3) >> 1) + (row >> 2)) + 4 * (row & 1);
-    const int koff = T::BLK * g4 + lane_ofs;
-    const int voff = T::BLK * ((4 * g4) / T::VROWS) + 64 * (((4 * g4) % T::VROWS) >> 2) + lane_ofs;
-
     const int tb0 = kst & ~7;
     const int ntiles = ntok > 0 ? (kend - tb0 + T::TT - 1) / T::TT : 0;
     const int nsteps = ntok > 0 ? (kend - tb0 + 31) / 32 : 0;
-    auto stage = [&](int g) { return lds + ((g >> 1) & (STAGES - 1)) * T::ELEMS; };
+    auto tile_stage = [&](int t) { return lds + (t % STAGES) * T::ELEMS; };
+    auto stage = [&](int g) { return tile_stage(g >> 1); };  // stage of step g's tile
 
-    // prologue: tiles 0-2 in flight, wait for tile 0, stage step 0's scores
-    for (int t = 0; t < 3 && t < ntiles; ++t)
-        TM::copy(lds + t * T::ELEMS, p.kp, p.vp, h, p.tcap, tb0 + t * T::TT, kst, kend, wave, lane);
-    if (ntiles >= 3)
-        __builtin_amdgcn_s_waitcnt(TA_VMCNT(2 * BPW));
-    else if (ntiles == 2)
-        __builtin_amdgcn_s_waitcnt(TA_VMCNT(BPW));
-    else
-        __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
+    // Attached private segments (xtail record of this item: count, then
+    // (first token, tokens, first job row) per segment) follow the job's own
+    // tiles in one tile sequence through the same LDS stages.
+    // read through the constant address space: scalar loads (the record is not written during the launch)
+    const __attribute__((address_space(4))) int32_t *xt =
+        p.xtail ? (const __attribute__((address_space(4))) int32_t *)(p.xtail + (size_t)item * p.xtail_stride)
+                : nullptr;
+    const int nx = xt ? xt[0] : 0;
+    auto seg_span = [&](int k, int &xs, int &xe) {  // clamped token range of segment k
+        xs = xt[1 + 3 * k];
+        xe = xs + max(0, min(xt[2 + 3 * k], p.tcap - xs));
+    };
+    auto seg_tiles = [&](int xs, int xe) { return xe > xs ? (xe - (xs & ~7) + T::TT - 1) / T::TT : 0; };
+    int ntot = ntiles;
+    for (int k = 0; k < nx; ++k) {
+        int xs, xe;
+        seg_span(k, xs, xe);
+        ntot += seg_tiles(xs, xe);
+    }
+    // copy tile t of the sequence into stage st
+    auto copy_tile = [&](int t, u16 *st) {
+        if (t < ntiles) {
+            TM::copy(st, p.kp, p.vp, h, p.tcap, tb0 + t * T::TT, kst, kend, wave, lane);
+            return;
+        }
+        int rem = t - ntiles;
+        for (int k = 0; k < nx; ++k) {
+            int xs, xe;
+            seg_span(k, xs, xe);
+            const int n = seg_tiles(xs, xe);
+            if (rem < n) {
+                TM::copy(st, p.kp, p.vp, h, p.tcap, (xs & ~7) + rem * T::TT, xs, xe, wave, lane);
+                return;
+            }
+            rem -= n;
+        }
+    };
+
+    // Prologue.  Loads retire in order, and a wait for a load's result also
+    // waits for every copy issued before it, so the dependent chain
+    // (request ids -> Q rows) is kept short: tile 0's copies go out with the
+    // request-id loads (both are needed before the first step), then all Q
+    // loads at once (every lane loads a valid row, rows past the job are
+    // zeroed afterwards), and tiles 1 .. STAGES-2 once Q has landed.
+    if (ntot > 0) copy_tile(0, lds);
+    int rq[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int rr = max(0, min(wrow0 + 16 * nb + row, nrows - 1));
+        rq[nb] = p.qids[(size_t)job * p.maxr + rr / p.group];
+    }
+    u32x4 qf[NB][KS];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int rr = max(0, min(wrow0 + 16 * nb + row, nrows - 1));
+        const u16 *src = p.q + ((size_t)rq[nb] * p.hq + h * p.group + rr % p.group) * D + 8 * g4;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) qf[nb][k] = *(const u32x4 *)(src + 32 * k);
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const bool valid = wrow0 + 16 * nb + row < nrows;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            if (!valid) qf[nb][k] = u32x4{0, 0, 0, 0};
+            asm volatile("" : "+v"(qf[nb][k]));
+        }
+    }
+    for (int t = 1; t < STAGES - 1 && t < ntot; ++t) copy_tile(t, tile_stage(t));
+
+    M acc;
+    acc.reset();
+    const LdsOfs of = T::offsets(row, g4);
+
+    wait_tiles<BPW>(min(ntot, STAGES - 1) - 1);  // tile 0 landed (tiles 1 .. STAGES-2 may be in flight)
     __builtin_amdgcn_s_barrier();
     if (active && nsteps > 0) {
         f32x4 s0[NB][2];
-        TM::load_k(lds, koff, 0, acc.kf);
+        TM::load_k(lds, of, 0, acc.kf);
         TM::qk(acc.kf, qf, s0);
         acc.template finish_scores<true>(s0, kst - tb0, kend - tb0, g4);
         acc.rescale(c, rc);
-        if (nsteps > 1) TM::load_k(lds, koff, 32, acc.kf);
+        if (nsteps > 1) TM::load_k(lds, of, 32, acc.kf);
     }
 
     // Entering tile t (at step 2t): tile t+1 must have landed, since this
-    // tile's first block reads its K; once every wave passed the barrier the
-    // stage of tile t-1 is free for tile t+3.
+    // tile's first block reads its K (tiles t+2 .. t+STAGES-2 may still be in
+    // flight); once every wave passed the barrier the stage of tile t-1 is
+    // free for tile t+STAGES-1.
     auto sync_tile = [&](int t) {
-        if (t + 1 >= ntiles) return;
-        if (t + 2 < ntiles)
-            __builtin_amdgcn_s_waitcnt(TA_VMCNT(BPW));
-        else
-            __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
+        if (t + 1 >= ntot) return;
+        wait_tiles<BPW>(min(t + STAGES - 2, ntot - 1) - (t + 1));
         __builtin_amdgcn_s_barrier();
-        if (t + 3 < ntiles)
-            TM::copy(lds + ((t + 3) & (STAGES - 1)) * T::ELEMS, p.kp, p.vp, h, p.tcap, tb0 + (t + 3) * T::TT, kst,
-                     kend, wave, lane);
+        if (t + STAGES - 1 < ntot) copy_tile(t + STAGES - 1, tile_stage(t + STAGES - 1));
     };
     // steady state: steps whose successor is neither the last nor masked
     int g = 0;
@@ -606,7 +716,7 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
         if (!(g & 1)) sync_tile(g >> 1);
         if (active) {
             const int gk = g + 2;
-            acc.template block<true, false>(stage(g), 32 * (g & 1), stage(gk), 32 * (gk & 1), qf, koff, voff, 0, 32,
+            acc.template block<true, false>(stage(g), 32 * (g & 1), stage(gk), 32 * (gk & 1), qf, of, 0, 32,
                                             g4, c);
             acc.rescale(c, rc);
         }
@@ -614,21 +724,46 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     // the last two steps: the successor of step nsteps-2 may be masked at its end
     if (g + 1 < nsteps) {
         if (!(g & 1)) sync_tile(g >> 1);
-        if (active) {
-            const int hi = kend - (tb0 + 32 * (g + 1));
-            if (hi < 32)
-                acc.template block<true, true>(stage(g), 32 * (g & 1), stage(g + 1), 32 * ((g + 1) & 1), qf, koff,
-                                               voff, 0, hi, g4, c);
-            else
-                acc.template block<true, false>(stage(g), 32 * (g & 1), stage(g + 1), 32 * ((g + 1) & 1), qf, koff,
-                                                voff, 0, 32, g4, c);
+        if (active) {  // one (masked) form for either end of the job keeps the register allocation simple
+            acc.template block<true, true>(stage(g), 32 * (g & 1), stage(g + 1), 32 * ((g + 1) & 1), qf, of,
+                                           0, kend - (tb0 + 32 * (g + 1)), g4, c);
             acc.rescale(c, rc);
         }
         ++g;
     }
     if (g < nsteps) {
         if (!(g & 1)) sync_tile(g >> 1);
-        if (active) acc.template block<false, false>(stage(g), 32 * (g & 1), stage(g), 0, qf, koff, voff, 0, 32, g4, c);
+        if (active) acc.template block<false, false>(stage(g), 32 * (g & 1), stage(g), 0, qf, of, 0, 32, g4, c);
+    }
+
+    // Attached segments, in rounds of up to STAGES tiles that are resident
+    // together: one wait and one barrier per round, then every wave attends
+    // the round's tiles of the segments holding its rows, side by side.  The
+    // root loop already issued the first tiles (up to ntiles + STAGES - 2).
+    {
+        int issued = min(ntiles + STAGES - 1, ntot);
+        for (int r0 = ntiles; r0 < ntot; r0 += STAGES) {
+            const int r1 = min(r0 + STAGES, ntot);
+            __builtin_amdgcn_s_barrier();  // every wave is done with the tiles before r0
+            for (; issued < r1; ++issued) copy_tile(issued, tile_stage(issued));
+            __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
+            __builtin_amdgcn_s_barrier();  // the round's tiles landed
+            int u = ntiles;  // sequence index of segment k's first tile
+            for (int k = 0; k < nx && u < r1; ++k) {
+                int xs, xe;
+                seg_span(k, xs, xe);
+                const int n = seg_tiles(xs, xe), xb = xs & ~7;
+                const int rlo = xt[3 + 3 * k] - wrow0;  // segment rows in this wave: [rlo, rlo + group)
+                if (active && rlo >= 0 && rlo < 16 * NB) {
+                    for (int i = max(0, r0 - u); i < n && u + i < r1; ++i) {
+                        const int t0 = xb + i * T::TT;
+                        acc.tail_tile(tile_stage(u + i), qf, of, max(0, xs - t0),
+                                      min(T::TT, xe - t0), rlo, rlo + p.group, row, g4, c, rc);
+                    }
+                }
+                u += n;
+            }
+        }
     }
 
     if (!active) return;
@@ -693,14 +828,12 @@ __global__ __launch_bounds__(128) void seg_tail_kernel(SegParams p) {
         }
         M acc;
         acc.reset();
-        const int lane_ofs = 8 * (4 * ((row & 3) >> 1) + (row >> 2)) + 4 * (row & 1);
-        const int koff = T::BLK * g4 + lane_ofs;
-        const int voff = T::BLK * ((4 * g4) / T::VROWS) + 64 * (((4 * g4) % T::VROWS) >> 2) + lane_ofs;
+        const LdsOfs of = T::offsets(row, g4);
         for (int it = 0; it < ntiles; ++it) {
             const int t0 = tb0 + it * T::TT;
             if (it > 0) M::copy(lds, p.kp, p.vp, h, p.tcap, t0, kst, kend, 0, lane);
             __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
-            acc.tile(lds, qf, koff, voff, max(0, kst - t0), min(T::TT, kend - t0), g4, p.scale_log2);
+            acc.tile(lds, qf, of, max(0, kst - t0), min(T::TT, kend - t0), g4, p.scale_log2);
         }
         // the tile's reads fed the MFMAs above, so the stage is free for the partial
         const bool any = acc.m[0] != NEG_INF;

@@ -140,6 +140,11 @@ struct SegParams {
     const int32_t *slots, *counts;
     u16 *out;
     int maxs;
+    // TA_LARGE256 items only (nullable): per item xtail_stride ints -- the
+    // number of attached private segments, then (first token, tokens, first
+    // job row) of each; the item folds them into its rows' partials
+    const int32_t *xtail;
+    int xtail_stride;
 };
 
 // Kernel timing hook (ta_time_next_launch): when set, the next kernel this

@@ -434,10 +434,10 @@ __global__ __launch_bounds__(64 * NW) void seg_large_kernel(SegParams p) {
 // One workgroup per (request, group of MH query heads); thread (head, d4)
 // owns four head-dim elements of one query head.  The slot list is uniform
 // per workgroup (scalar loads), and each thread reads the log-sum-exp and the
-// 16-byte partial slice of CHUNK slots at once and merges them online in
-// registers: slots -> (lse, partials) is the only chain of dependent memory
-// round trips; no LDS and no barriers.
-constexpr int MERGE_CHUNK = 8;
+// 8-byte partial slice (four fp16 values) of MERGE_CHUNK slots at once and
+// merges them online in registers: slots -> (lse, partials) is the only chain
+// of dependent memory round trips; no LDS and no barriers.
+constexpr int MERGE_CHUNK = 16;
 
 template <int D, bool FP16>
 __global__ __launch_bounds__(NT) void merge_kernel(const u16 *__restrict__ part, const float *__restrict__ lse,
@@ -584,7 +584,8 @@ int segment_launch(const void *q, const void *kp, const void *vp, const int32_t 
                    const int32_t *qlen, const int32_t *klen, const int32_t *rowbase, const int32_t *items,
                    int32_t n_items, int32_t kind, void *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
                    int32_t d, int32_t tcap, int32_t maxr, int32_t dtype, const int32_t *slots,
-                   const int32_t *counts, void *out, int32_t maxs, void *stream) {
+                   const int32_t *counts, void *out, int32_t maxs, const int32_t *xtail, int32_t xtail_stride,
+                   void *stream) {
     if (int e = check_common(hq, hk, d, dtype)) return e;
     if (n_items < 0 || nreq <= 0 || tcap <= 0 || maxr <= 0 || kind < TA_SMALL || kind > TA_TAIL) return TA_ERR_ARG;
     if (n_items == 0) return 0;
@@ -597,6 +598,12 @@ int segment_launch(const void *q, const void *kp, const void *vp, const int32_t 
 #endif
         if (kind != TA_TAIL || tcap % 8 != 0 || !slots || !counts || maxs <= 0) return TA_ERR_ARG;
         if (!aligned16(out)) return TA_ERR_ALIGN;
+    }
+    if (xtail) {
+#ifdef TA_LEGACY_LARGE
+        return TA_ERR_ARG;  // the register-staged kernels take no attached segments
+#endif
+        if (kind != TA_LARGE256 || tcap % 8 != 0 || xtail_stride < 1) return TA_ERR_ARG;
     }
     SegParams sp;
     sp.q = static_cast<const u16 *>(q);
@@ -621,6 +628,8 @@ int segment_launch(const void *q, const void *kp, const void *vp, const int32_t 
     sp.counts = counts;
     sp.out = static_cast<u16 *>(out);
     sp.maxs = maxs;
+    sp.xtail = xtail;
+    sp.xtail_stride = xtail_stride;
     const hipStream_t st = static_cast<hipStream_t>(stream);
 #define TA_SEG(D, F) launch_segment<D, F>(sp, kind, st)
     return (int)TA_DISPATCH(d, dtype == TA_FP16, TA_SEG);
@@ -629,10 +638,11 @@ int segment_launch(const void *q, const void *kp, const void *vp, const int32_t 
 
 int plan_segment(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan, int kind,
                  void *out, void *stream) {
+    const bool xt = kind == TA_LARGE256 && plan->xtail;
     return segment_launch(q, kp, vp, plan->qids, plan->kstart, plan->qlen, plan->klen, plan->rowbase,
                           plan->items[kind], plan->n_items[kind], kind, plan->part, plan->lse, plan->nreq, plan->hq,
                           plan->hk, plan->d, tcap, plan->maxr, plan->dtype, plan->slots, plan->counts, out,
-                          plan->maxs, stream);
+                          plan->maxs, xt ? plan->xtail : nullptr, xt ? plan->xtail_stride : 0, stream);
 }
 
 }  // namespace
@@ -644,7 +654,7 @@ int ta_segment(const void *q, const void *kp, const void *vp, const int32_t *qid
                int32_t n_items, int32_t kind, void *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
                int32_t d, int32_t tcap, int32_t maxr, int32_t dtype, void *stream) {
     return segment_launch(q, kp, vp, qids, kstart, qlen, klen, rowbase, items, n_items, kind, part, lse, nreq, hq,
-                          hk, d, tcap, maxr, dtype, nullptr, nullptr, nullptr, 0, stream);
+                          hk, d, tcap, maxr, dtype, nullptr, nullptr, nullptr, 0, nullptr, 0, stream);
 }
 
 int ta_merge(const void *part, const float *lse, const int32_t *slots, const int32_t *counts, void *out,
@@ -657,6 +667,12 @@ int ta_merge(const void *part, const float *lse, const int32_t *slots, const int
 #define TA_MRG(D, F) launch_merge<D, F>(part, lse, slots, counts, nullptr, out, nreq, hq, maxs, st)
     return (int)TA_DISPATCH(d, dtype == TA_FP16, TA_MRG);
 #undef TA_MRG
+}
+
+int ta_segment_plan(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan, int32_t kind,
+                    void *stream) {
+    if (!plan || kind < TA_SMALL || kind > TA_TAIL) return TA_ERR_ARG;
+    return plan_segment(q, kp, vp, tcap, plan, kind, nullptr, stream);
 }
 
 int ta_tail_merge(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan, void *out,
@@ -673,6 +689,8 @@ int ta_attention_matrix(const void *q, const void *kp, const void *vp, int32_t t
 #else
     const bool fused = tcap % 8 == 0;  // the LDS-transpose kernels carry the fused merge
 #endif
+    // attached segments exist only on the LDS-transpose path (pools with tcap % 8 == 0)
+    if (plan->xtail && !fused) return TA_ERR_ARG;
     // the partials every merge reads come first: large jobs, then small jobs
     static const int order[] = {TA_LARGE256, TA_LARGE128, TA_LARGE64, TA_SMALL};
     for (int kind : order) {
@@ -688,7 +706,9 @@ int ta_attention_matrix(const void *q, const void *kp, const void *vp, int32_t t
     if (plan->n_items[TA_TAIL] > 0)
         if (int e = plan_segment(q, kp, vp, tcap, plan, TA_TAIL, out, stream)) return e;
     if (plan->n_rest <= 0) return 0;
-    if (!plan->rest || !plan->part || !plan->lse || !plan->slots || !plan->counts) return TA_ERR_ARG;
+    // rest == NULL with n_rest == nreq: every request
+    if ((!plan->rest && plan->n_rest != plan->nreq) || !plan->part || !plan->lse || !plan->slots || !plan->counts)
+        return TA_ERR_ARG;
     if (plan->dtype != TA_BF16 && plan->dtype != TA_FP16) return TA_ERR_DTYPE;
     if (plan->maxs <= 0 || (plan->d != 32 && plan->d != 64 && plan->d != 128)) return TA_ERR_ARG;
     if (!aligned16(plan->part) || !aligned16(out)) return TA_ERR_ALIGN;

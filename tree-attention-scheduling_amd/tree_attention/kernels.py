@@ -69,6 +69,39 @@ class PreparedPlan:
     abi: _native.TaPlan | None = None
     metadata: torch.Tensor | None = None
     rest: torch.Tensor | None = None  # requests the merge kernel covers (no TA_TAIL job)
+    # private segments folded into TA_LARGE256 work items: {(job, first row): [(Job, first job row)]}
+    attached: dict = field(default_factory=dict)
+    xtail: torch.Tensor | None = None
+    plan: Plan | None = None
+    options: dict = field(default_factory=dict)  # prepare's tile_rows / fixed_from
+    growing_len: int | None = None  # last CachedDecodePlan.update length of the growing jobs
+    _unattached: "PreparedPlan | None" = None
+
+    def fill_growing(self, length: int) -> None:
+        """Set ``klen`` of the growing jobs (tokens from ``fixed_from`` on) to
+        ``length``, here and in the unattached variant (device-side, no sync)."""
+        start = self.options.get("fixed_from")
+        idx = [i for i, job in enumerate(self.jobs) if start is not None and job.tokens[0] >= start]
+        if idx:
+            self.klen.index_fill_(0, torch.tensor(idx, device=self.klen.device), length)
+        self.growing_len = length
+        if self._unattached is not None:
+            self._unattached.fill_growing(length)
+
+    def for_pools(self, kp: torch.Tensor) -> "PreparedPlan":
+        """The plan to launch on pools like ``kp``: this one, or, when it has
+        attached segments and the pool capacity is not a multiple of 8 (the
+        register-staged kernels, which take no attachments), the same plan
+        prepared without attachments, writing into the same ``out``."""
+        if not self.attached or kp.shape[-1] % 8 == 0:
+            return self
+        if self._unattached is None:
+            alt = prepare(self.plan, self.out, attach_tails=False, **self.options)
+            alt.out = self.out
+            if self.growing_len is not None:
+                alt.fill_growing(self.growing_len)
+            self._unattached = alt
+        return self._unattached
 
 
 def _tail_jobs(jobs, small_jobs):
@@ -107,6 +140,66 @@ def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256, tails=frozense
 
 
 TOKEN_QUANTUM = 64  # tokens per LDS tile of the segment kernels
+XTAIL_MAX = 8       # private segments one TA_LARGE256 work item takes on
+WAVE_ROWS = 32      # query rows of one wave of the TA_LARGE256 kernel
+
+
+def _tiles(job) -> int:
+    """LDS tiles the segment kernels stream for ``job``'s token run."""
+    t0 = job.tokens[0]
+    return -(-(t0 + len(job.tokens) - (t0 & ~7)) // TOKEN_QUANTUM)
+
+
+def _attach_tails(small, large, group, tile_rows, is_fixed):
+    """Fold single-request small jobs into TA_LARGE256 work items of large jobs.
+
+    A small job of one request ``r`` (a private tail) can be attended by any
+    256-row work item of a large job whose rows include ``r``'s: the wave that
+    holds those rows attends the tail's tokens into the same online-softmax
+    state, so the item's partial for ``r`` covers the job's tokens and the
+    tail's, and the tail needs no launch, work item or partial slot of its own.
+    Each tail goes to the candidate item with the fewest attached tiles (then
+    the fewest on the owning wave, then the first job), up to ``XTAIL_MAX``
+    segments per item and no more attached tiles than the item's own, so the
+    large kernel's items stay balanced.  Tails for which ``is_fixed`` holds
+    (growing decode tails) are not attached.
+
+    Returns the small jobs left and ``{(large job index, first row): [(job, first job row)]}``.
+    """
+    holders = {}
+    for J, job in enumerate(large):
+        rows = len(job.requests) * group
+        if _large_kind(rows, tile_rows) != _native.TA_LARGE256:
+            continue
+        for pos, r in enumerate(job.requests):
+            holders.setdefault(r, []).append((J, pos * group))
+    attached, item_tiles, wave_tiles = {}, {}, {}
+    left = []
+    for job in small:
+        r = job.requests[0]
+        if len(job.requests) != 1 or is_fixed(job) or r not in holders:
+            left.append(job)
+            continue
+        n = _tiles(job)
+        best = None
+        for J, lrow in holders[r]:
+            if lrow % WAVE_ROWS + group > WAVE_ROWS:
+                continue  # the request's rows must lie in one wave
+            key = (J, lrow // 256 * 256)
+            wave = (lrow - key[1]) // WAVE_ROWS
+            if len(attached.get(key, ())) >= XTAIL_MAX or item_tiles.get(key, 0) + n > _tiles(large[J]):
+                continue
+            score = (item_tiles.get(key, 0), wave_tiles.get(key + (wave,), 0), J)
+            if best is None or score < best[0]:
+                best = (score, key, wave, lrow)
+        if best is None:
+            left.append(job)
+            continue
+        _, key, wave, lrow = best
+        attached.setdefault(key, []).append((job, lrow))
+        item_tiles[key] = item_tiles.get(key, 0) + n
+        wave_tiles[key + (wave,)] = wave_tiles.get(key + (wave,), 0) + n
+    return left, attached
 
 
 def _recut(jobs, items_per_chunk, target_items, is_fixed):
@@ -155,7 +248,8 @@ def _cu_count(device) -> int:
     return 256  # MI355X
 
 
-def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int | None = None) -> PreparedPlan:
+def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int | None = None,
+            attach_tails: bool = True) -> PreparedPlan:
     """Lower ``plan`` to device metadata and scratch for queries shaped like ``q``.
 
     Mirrors kernels.py:103-141: physical jobs, stable small-first order, one
@@ -164,7 +258,10 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     large-job kernels handles; it changes the work split, not the result.
     Runs of jobs over one request group are re-cut for the GPU (``_recut``), so
     ``jobs`` holds the execution jobs; ``fixed_from`` keeps jobs whose tokens
-    start at or after it (decode tails whose length changes) as they are.  Raises
+    start at or after it (decode tails whose length changes) as they are.
+    ``attach_tails`` folds private single-request jobs into the 256-row work
+    items of the large jobs holding their request (``_attach_tails``); those
+    tails are then in ``attached``, not in ``jobs``.  Raises
     ``ValueError`` for jobs without requests or tokens, request ids outside
     ``q`` and token runs that are not consecutive physical ids.
     """
@@ -191,6 +288,11 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     def growing(job):
         return fixed_from is not None and job.tokens[0] >= fixed_from
 
+    large = _recut(large, lambda r: -(-len(r) * group // _native.KIND_ROWS[_large_kind(len(r) * group, tile_rows)])
+                   * kvheads, n_cu, growing)
+    attached = {}
+    if attach_tails:
+        small, attached = _attach_tails(small, large, group, tile_rows, growing)
     # Tails (a request's only small job) stay whole when they alone fill the GPU,
     # so that their work items can merge their requests.
     owners = {}
@@ -200,8 +302,6 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     tails = [j for j in small if len(j.requests) == 1 and owners[j.requests[0]] == 1]
     keep = {id(j) for j in tails} if len(tails) * kvheads >= n_cu else set()
     small = _recut(small, lambda r: kvheads, 8 * n_cu, lambda j: growing(j) or id(j) in keep)
-    large = _recut(large, lambda r: -(-len(r) * group // _native.KIND_ROWS[_large_kind(len(r) * group, tile_rows)])
-                   * kvheads, n_cu, growing)
     jobs = small + large
     small_jobs = len(small)
     njobs = len(jobs)
@@ -238,16 +338,27 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     items = _build_items(jobs, small_jobs, group, kvheads, tile_rows, tails)
     tail_requests = {jobs[j].requests[0] for j in tails}
     rest = np.array([r for r in range(nreq) if r not in tail_requests], dtype=np.int32)
+    # attached segments of each TA_LARGE256 item: count, then (first token, tokens, first job row)
+    xstride = 1 + 3 * XTAIL_MAX
+    big = items[_native.TA_LARGE256].reshape(-1, 3)
+    xtail = np.zeros((len(big), xstride), dtype=np.int32)
+    for i, (j, row0, _) in enumerate(big.tolist()):
+        segs = attached.get((j - small_jobs, row0), ())
+        xtail[i, 0] = len(segs)
+        for k, (job, lrow) in enumerate(segs):
+            xtail[i, 1 + 3 * k: 4 + 3 * k] = (job.tokens[0], len(job.tokens), lrow)
+    if not attached:
+        xtail = np.zeros((0, xstride), dtype=np.int32)
 
-    arrays = [qids, kids, qlen, klen, slot_array, counts, rowbase, rest] + [items[k] for k in sorted(items)]
+    arrays = [qids, kids, qlen, klen, slot_array, counts, rowbase, rest, xtail] + [items[k] for k in sorted(items)]
     dev = q.device
     metadata = torch.from_numpy(np.concatenate([a.ravel() for a in arrays])).to(dev)
     views, offset = [], 0
     for array in arrays:
         views.append(metadata[offset:offset + array.size].view(array.shape))
         offset += array.size
-    qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t, rest_t = views[:8]
-    item_views = dict(zip(sorted(items), views[8:]))
+    qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t, rest_t, xtail_t = views[:9]
+    item_views = dict(zip(sorted(items), views[9:]))
     contiguous_q = all(j.requests[-1] - j.requests[0] + 1 == len(j.requests) for j in jobs)
     # partial rows: fp16 scaled by 2^-e per row; lse holds (log-sum-exp, e) per row
     part = torch.empty((nslot, hq, dim), device=dev, dtype=torch.float16)
@@ -261,13 +372,19 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     for kind, view in item_views.items():
         abi.items[kind] = view.data_ptr() if view.numel() else None
         abi.n_items[kind] = view.numel() // 3
-    abi.rest, abi.n_rest = (rest_t.data_ptr() if rest.size else None), int(rest.size)
+    # rest = every request: the merge takes requests 0..nreq-1 directly (one dependent load less)
+    every = rest.size == nreq
+    abi.rest, abi.n_rest = (rest_t.data_ptr() if rest.size and not every else None), int(rest.size)
     abi.part, abi.lse = part.data_ptr(), lse.data_ptr()
     abi.njobs, abi.maxr, abi.maxs, abi.nreq, abi.nslot = njobs, maxr, maxs, nreq, nslot
     abi.hq, abi.hk, abi.d = hq, kvheads, dim
     abi.dtype = _DTYPES.get(q.dtype, -1)
+    abi.xtail, abi.xtail_stride = (xtail_t.data_ptr(), xstride) if attached else (None, 0)
+    keyed = {(j + small_jobs, row0): segs for (j, row0), segs in attached.items()}
     return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
-                        slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t)
+                        slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t,
+                        keyed, xtail_t if attached else None, plan,
+                        {"tile_rows": tile_rows, "fixed_from": fixed_from})
 
 
 def pack_kv(k: torch.Tensor, v: torch.Tensor):
@@ -304,8 +421,8 @@ def attention_matrix(q, kp, vp, prepared):
     Returns ``prepared.out`` (``[R, HQ, D]`` in q's dtype), which every call
     overwrites, as in the reference.
     """
-    p = prepared
-    _check_inputs(q, kp, vp, p)
+    _check_inputs(q, kp, vp, prepared)
+    p = prepared.for_pools(kp)
     if not q.is_contiguous():
         q = q.contiguous()
     lib = _native.load()
@@ -314,30 +431,27 @@ def attention_matrix(q, kp, vp, prepared):
         rc = lib.ta_attention_matrix(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), kp.shape[2],
                                      ctypes.byref(p.abi), p.out.data_ptr(), stream)
     _native.check(rc)
-    return p.out
+    return prepared.out
 
 
 def segment(q, kp, vp, prepared, kind: int):
     """Launch one segment phase (``kind`` = TA_SMALL / TA_LARGE64/128/256 / TA_TAIL) of a plan.
 
     Every kind writes partials here, TA_TAIL included; ``merge`` then combines
-    all requests.
+    all requests.  TA_LARGE256 items attend their attached segments too.
 
     Counterpart of the direct ``_segment`` launches in the reference's
     scripts/calibrate_tiles.py:24-29 and scripts/profile_kernel.py:17-20.
     """
-    p = prepared
-    _check_inputs(q, kp, vp, p)
-    abi = p.abi
-    n = abi.n_items[kind]
-    if n == 0:
+    _check_inputs(q, kp, vp, prepared)
+    p = prepared.for_pools(kp)
+    if p.abi.n_items[kind] == 0:
         return
     lib = _native.load()
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        rc = lib.ta_segment(q.contiguous().data_ptr(), kp.data_ptr(), vp.data_ptr(), abi.qids, abi.kstart,
-                            abi.qlen, abi.klen, abi.rowbase, abi.items[kind], n, kind, abi.part, abi.lse,
-                            abi.nreq, abi.hq, abi.hk, abi.d, kp.shape[2], abi.maxr, abi.dtype, stream)
+        rc = lib.ta_segment_plan(q.contiguous().data_ptr(), kp.data_ptr(), vp.data_ptr(), kp.shape[2],
+                                 ctypes.byref(p.abi), kind, stream)
     _native.check(rc)
 
 
@@ -358,9 +472,13 @@ def tail_merge(q, kp, vp, prepared):
     return p.out
 
 
-def merge(prepared):
-    """Launch the log-sum-exp merge of a plan's partials into ``prepared.out`` (kernels.py:166-167)."""
-    p = prepared
+def merge(prepared, kp=None):
+    """Launch the log-sum-exp merge of a plan's partials into ``prepared.out`` (kernels.py:166-167).
+
+    ``kp``: the pools the partials were computed on (selects the plan variant,
+    see ``PreparedPlan.for_pools``); default: pools with a capacity multiple of 8.
+    """
+    p = prepared if kp is None else prepared.for_pools(kp)
     abi = p.abi
     lib = _native.load()
     with torch.cuda.device(p.out.device):
@@ -417,4 +535,7 @@ class CachedDecodePlan:
         if not 0 <= generated_tokens <= self.max_new_tokens:
             raise ValueError("generated_tokens must be within [0, max_new_tokens]")
         self.prepared.klen.index_fill_(0, self.tail_indices, generated_tokens)
+        self.prepared.growing_len = generated_tokens
+        if self.prepared._unattached is not None:
+            self.prepared._unattached.fill_growing(generated_tokens)
         return self.prepared

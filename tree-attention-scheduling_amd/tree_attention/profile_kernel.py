@@ -9,18 +9,21 @@ merging their requests, as in the layer), ``merge``, ``layer`` (the whole attent
 device-to-device copy of ``--copy-mib`` MiB, the reference point that scales
 rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes).  K/V rotate over
 ``--pools`` copies so repeated launches read HBM, not the MALL.  Prints the
-mean device time per launch measured with HIP events.
+mean device time per launch measured with HIP events (launch gaps included)
+and, with ``--stamp``, the median of the kernels' own durations (dispatch
+begin/end stamps of each launch through ``ta_time_next_launch``).
 """
 from __future__ import annotations
 
 import argparse
 import json
+import statistics
 
 import torch
 
 from . import CostModel, schedule, shapes
 from . import _native
-from .kernels import attention_matrix, merge, pack_kv, prepare, segment, tail_merge
+from .kernels import attention_matrix, launch_durations_us, merge, pack_kv, prepare, segment, tail_merge
 
 KINDS = {"small": _native.TA_SMALL, "large64": _native.TA_LARGE64, "large128": _native.TA_LARGE128,
          "large256": _native.TA_LARGE256, "tail": _native.TA_TAIL}
@@ -39,6 +42,8 @@ def main(argv=None):
     ap.add_argument("--pools", type=int, default=8)
     ap.add_argument("--heads", default="32,8,128")
     ap.add_argument("--tile-rows", type=int, default=256)
+    ap.add_argument("--stamp", action="store_true",
+                    help="also report the median kernel duration from dispatch stamps (library kernels only)")
     ap.add_argument("--param", action="append", default=[],
                     help="CostModel field override, e.g. --param kv_split=1024 (repeatable)")
     args = ap.parse_args(argv)
@@ -90,10 +95,13 @@ def main(argv=None):
         launch(i)
     end.record()
     torch.cuda.synchronize()
-    print(json.dumps({"kernel": args.kernel, "shape": args.shape, "method": args.method,
-                      "params": {f: getattr(model, f) for f in ("kv_split", "max_query_rows")},
-                      "tile_rows": args.tile_rows, "iters": args.iters, "us_per_launch": start.elapsed_time(end) * 1e3 / args.iters,
-                      "items": list(prepared.abi.n_items)}), flush=True)
+    row = {"kernel": args.kernel, "shape": args.shape, "method": args.method,
+           "params": {f: getattr(model, f) for f in ("kv_split", "max_query_rows")},
+           "tile_rows": args.tile_rows, "iters": args.iters, "us_per_launch": start.elapsed_time(end) * 1e3 / args.iters,
+           "items": list(prepared.abi.n_items)}
+    if args.stamp and args.kernel != "copy":
+        row["kernel_us_median"] = statistics.median(launch_durations_us(launch, args.iters))
+    print(json.dumps(row), flush=True)
 
 
 if __name__ == "__main__":
