@@ -55,6 +55,10 @@ extern "C" {
                            is the last of its request's slots. */
 #define TA_NKINDS 5
 
+/* attached private segments per TA_LARGE256 work item (ta_plan.xtail) */
+#define TA_XTAIL_MAX 4
+#define TA_XTAIL_STRIDE (1 + 3 * TA_XTAIL_MAX)
+
 #define TA_ERR_ARG 1001      /* null pointer, bad size or unsupported shape */
 #define TA_ERR_ALIGN 1002    /* q / kp / vp / part / out not 16-byte aligned */
 #define TA_ERR_DTYPE 1003    /* dtype not TA_BF16 / TA_FP16 */
@@ -80,15 +84,20 @@ typedef struct ta_plan {
     int32_t hq, hk, d, dtype;
     int32_t n_rest;
     /* Attached private segments of the TA_LARGE256 items (NULL: none), an
-     * execution detail with no counterpart in the reference: xtail_stride ints
-     * per TA_LARGE256 item -- the number of segments n, then (first physical
-     * token, tokens, first job row) for each of the n.  The segment's tokens
+     * execution detail with no counterpart in the reference: xtail_stride
+     * (= TA_XTAIL_STRIDE) ints per TA_LARGE256 item -- the number of segments
+     * n <= TA_XTAIL_MAX, then (first physical token, tokens, first job row)
+     * for each of the n.  The segment's tokens
      * belong to the request whose group query rows start at that job row
      * (rows of one wave, 32 rows); the item folds them into that request's
      * partial rows, so the segment has no partial slot of its own.  Needs
      * tcap % 8 == 0 (ta_attention_matrix returns TA_ERR_ARG otherwise). */
     const int32_t *xtail;
     int32_t xtail_stride;
+    /* [njobs] or NULL: the first request id of each job whose requests are
+     * consecutive (qids[j*maxr + i] == qbase[j] + i), -1 for the others
+     * (cf. the reference's contiguous-Q path, kernels.py:23-26, 138). */
+    const int32_t *qbase;
 } ta_plan;
 
 /* Version string of the library build. */

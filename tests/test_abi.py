@@ -61,3 +61,13 @@ def test_plan_struct_layout_matches_header(tmp_path):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="not found"):
         _native.load(tmp_path / "nope.so")
+
+
+def test_xtail_record_layout_matches_header():
+    """kernels.XTAIL_MAX and the record stride prepare writes equal TA_XTAIL_MAX / TA_XTAIL_STRIDE."""
+    import re
+    from pathlib import Path
+    from tree_attention import kernels
+    header = (Path(__file__).resolve().parents[1] / "include" / "tree_attn.h").read_text()
+    assert int(re.search(r"#define TA_XTAIL_MAX (\d+)", header).group(1)) == kernels.XTAIL_MAX
+    assert "#define TA_XTAIL_STRIDE (1 + 3 * TA_XTAIL_MAX)" in header

@@ -250,6 +250,34 @@ def test_attached_tails(hq, hk, d, dtype, pad, device):
     check(c, ref, 0.008, 0.03, "attached/segment+merge")
 
 
+def test_large_jobs_over_scattered_requests(device):
+    """256-row work items over requests that are not consecutive (the qids lookup) beside
+    consecutive ones (Q addressed from the first request id), with private tails."""
+    n = 160
+    jobs = [Job(tuple(range(0, n, 2)), tuple(range(0, 700))),     # even requests: 320 rows, qbase -1
+            Job(tuple(range(1, n, 2)), tuple(range(700, 1300))),  # odd requests
+            Job(tuple(range(0, 80)), tuple(range(1300, 1555)))]   # consecutive: qbase 0
+    jobs += [Job((r,), tuple(range(1560 + 9 * r, 1560 + 9 * r + 1 + r % 9))) for r in range(n)]
+    paths = [[] for _ in range(n)]
+    for job in jobs:
+        for r in job.requests:
+            paths[r].extend(job.tokens)
+    tree = _Paths([tuple(p) for p in paths])
+    g = torch.Generator().manual_seed(41)
+    q = torch.randn(n, 32, 128, generator=g).bfloat16()
+    k = torch.randn(1560 + 9 * n + 8, 8, 128, generator=g).bfloat16()
+    v = torch.randn(1560 + 9 * n + 8, 8, 128, generator=g).bfloat16()
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    prepared = prepare(Plan(jobs, "x", 0.0, dict(kvheads=8)), qd)
+    base = prepared.qbase_host
+    assert -1 in base and 0 in base
+    assert prepared.abi.n_items[_native.TA_LARGE256] > 0 and prepared.attached
+    out = attention_matrix(qd, kp, vp, prepared)
+    torch.cuda.synchronize()
+    check(out, oracle_fp32(q, k, v, tree), 0.008, 0.03, "scattered")
+
+
 @pytest.mark.parametrize("vscale", [1e5, 1e-5])
 def test_partial_rows_keep_range(vscale, device):
     """Partial rows are fp16 scaled by 2^-e per row: V far outside fp16's range

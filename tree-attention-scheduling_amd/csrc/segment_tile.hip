@@ -49,11 +49,12 @@ typedef __attribute__((address_space(3))) void lds_void;
 #define TA_VMCNT(n) ((((n)&15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
 
 // Wait until at most n tiles of this wave's copies (BPW each) are in flight
-// (n = 0 .. 3; the immediate of s_waitcnt must be a constant).
+// (n = 0 .. 4; the immediate of s_waitcnt must be a constant).
 template <int BPW>
 __device__ inline void wait_tiles(int n) {
-    static_assert(3 * BPW <= 63, "three tiles of copies fit the vmcnt counter");
+    static_assert(4 * BPW <= 63, "four tiles of copies fit the vmcnt counter");
     switch (n) {
+        case 4: __builtin_amdgcn_s_waitcnt(TA_VMCNT(4 * BPW)); break;
         case 3: __builtin_amdgcn_s_waitcnt(TA_VMCNT(3 * BPW)); break;
         case 2: __builtin_amdgcn_s_waitcnt(TA_VMCNT(2 * BPW)); break;
         case 1: __builtin_amdgcn_s_waitcnt(TA_VMCNT(BPW)); break;
@@ -428,9 +429,9 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
 // instructions alternate in each wave's instruction stream.  K/V tiles arrive
 // by LDS DMA into five stages: tiles t and t+1 are read while t+2 .. t+4 are
 // in flight, with one barrier per tile.
-template <int D, bool FP16, int NW>
+template <int D, bool FP16, int NW, int NB_ = 2>
 struct PipeMath {
-    static constexpr int NB = 2;
+    static constexpr int NB = NB_;
     static constexpr int DB = D / 16;
     static constexpr int KS = D / 32;
     using O = Ops<FP16>;
@@ -583,15 +584,20 @@ struct PipeMath {
 #define TA_PIPE_STAGES 5
 #endif
 
-template <int D, bool FP16, int NW, int STAGES = TA_PIPE_STAGES>
+// STAGES LDS tiles; the waves meet at a barrier every SYNC tiles.  While the
+// waves work on tiles t .. t+SYNC-1 they read those and the K of tile t+SYNC
+// (the pipelined steps read one step ahead), so SYNC+1 tiles are resident
+// and STAGES-SYNC-1 more can be in flight.
+template <int D, bool FP16, int NW, int NB = 2, int STAGES = TA_PIPE_STAGES, int SYNC = 1>
 __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     using T = Tile<D>;
-    using M = PipeMath<D, FP16, NW>;
-    using TM = TileMath<D, FP16, 2, NW>;
-    constexpr int NB = M::NB, KS = M::KS;
+    using M = PipeMath<D, FP16, NW, NB>;
+    using TM = TileMath<D, FP16, NB, NW>;
+    constexpr int KS = M::KS;
     constexpr int BPW = T::NBLK / NW;  // copies per wave per tile
     static_assert(T::NBLK % NW == 0, "every wave copies the same number of blocks");
-    static_assert(STAGES >= 4 && STAGES <= 5, "the pipelined steps read two tiles; up to three more in flight");
+    static_assert(SYNC >= 1 && STAGES >= 2 * SYNC + 1 && STAGES <= 5,
+                  "a group's tiles, the next K and the next group's copies fit the stages");
     __shared__ __attribute__((aligned(16))) u16 lds[STAGES * T::ELEMS];
 
     const int total = gridDim.x;
@@ -616,23 +622,32 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     auto stage = [&](int g) { return tile_stage(g >> 1); };  // stage of step g's tile
 
     // Attached private segments (xtail record of this item: count, then
-    // (first token, tokens, first job row) per segment) follow the job's own
-    // tiles in one tile sequence through the same LDS stages.
-    // read through the constant address space: scalar loads (the record is not written during the launch)
-    const __attribute__((address_space(4))) int32_t *xt =
-        p.xtail ? (const __attribute__((address_space(4))) int32_t *)(p.xtail + (size_t)item * p.xtail_stride)
-                : nullptr;
-    const int nx = xt ? xt[0] : 0;
-    auto seg_span = [&](int k, int &xs, int &xe) {  // clamped token range of segment k
-        xs = xt[1 + 3 * k];
-        xe = xs + max(0, min(xt[2 + 3 * k], p.tcap - xs));
-    };
-    auto seg_tiles = [&](int xs, int xe) { return xe > xs ? (xe - (xs & ~7) + T::TT - 1) / T::TT : 0; };
+    // (first token, tokens, first job row) for up to TA_XTAIL_MAX segments)
+    // follow the job's own tiles in one tile sequence through the same LDS
+    // stages.  The record is read at once (constant address space: one batch
+    // of scalar loads, no chain of dependent loads) into per-segment values
+    // that unrolled loops index with constants.
+    constexpr int XM = TA_XTAIL_MAX;
+    int rec[1 + 3 * XM];
+    if (p.xtail) {
+        const __attribute__((address_space(4))) int32_t *xt =
+            (const __attribute__((address_space(4))) int32_t *)(p.xtail + (size_t)item * p.xtail_stride);
+#pragma unroll
+        for (int i = 0; i < 1 + 3 * XM; ++i) rec[i] = xt[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 1 + 3 * XM; ++i) rec[i] = 0;
+    }
+    const int nx = min(max(rec[0], 0), XM);
+    int xs[XM], xe[XM], xfirst[XM], xn[XM];  // clamped token range, first tile and tiles of each segment
     int ntot = ntiles;
-    for (int k = 0; k < nx; ++k) {
-        int xs, xe;
-        seg_span(k, xs, xe);
-        ntot += seg_tiles(xs, xe);
+#pragma unroll
+    for (int k = 0; k < XM; ++k) {
+        xs[k] = max(0, rec[1 + 3 * k]);
+        xe[k] = xs[k] + max(0, min(rec[2 + 3 * k], p.tcap - xs[k]));
+        xn[k] = k < nx && xe[k] > xs[k] ? (xe[k] - (xs[k] & ~7) + T::TT - 1) / T::TT : 0;
+        xfirst[k] = ntot;
+        ntot += xn[k];
     }
     // copy tile t of the sequence into stage st
     auto copy_tile = [&](int t, u16 *st) {
@@ -640,31 +655,34 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
             TM::copy(st, p.kp, p.vp, h, p.tcap, tb0 + t * T::TT, kst, kend, wave, lane);
             return;
         }
-        int rem = t - ntiles;
-        for (int k = 0; k < nx; ++k) {
-            int xs, xe;
-            seg_span(k, xs, xe);
-            const int n = seg_tiles(xs, xe);
-            if (rem < n) {
-                TM::copy(st, p.kp, p.vp, h, p.tcap, (xs & ~7) + rem * T::TT, xs, xe, wave, lane);
-                return;
+        int t0n = 0, cs = 0, ce = 1;
+#pragma unroll
+        for (int k = 0; k < XM; ++k)
+            if (t >= xfirst[k] && t < xfirst[k] + xn[k]) {
+                t0n = (xs[k] & ~7) + (t - xfirst[k]) * T::TT;
+                cs = xs[k];
+                ce = xe[k];
             }
-            rem -= n;
-        }
+        TM::copy(st, p.kp, p.vp, h, p.tcap, t0n, cs, ce, wave, lane);
     };
 
     // Prologue.  Loads retire in order, and a wait for a load's result also
     // waits for every copy issued before it, so the dependent chain
-    // (request ids -> Q rows) is kept short: tile 0's copies go out with the
-    // request-id loads (both are needed before the first step), then all Q
-    // loads at once (every lane loads a valid row, rows past the job are
-    // zeroed afterwards), and tiles 1 .. STAGES-2 once Q has landed.
-    if (ntot > 0) copy_tile(0, lds);
+    // (request ids -> Q rows) is kept short.  A job over consecutive requests
+    // (qbase[job] >= 0, cf. the reference's contiguous-Q path,
+    // kernels.py:23-26) addresses its Q rows from the first request id, a
+    // scalar load beside the job's other metadata: the Q loads go out before
+    // tile 0's copies.  Otherwise tile 0's copies go out with the request-id
+    // loads (both are needed before the first step), then the Q loads.  Every
+    // lane loads a valid row (rows past the job are zeroed afterwards); tiles
+    // 1 .. STAGES-1 follow once Q has landed.
+    const int qb = p.qbase ? p.qbase[job] : -1;
     int rq[NB];
+    if (qb < 0 && ntot > 0) copy_tile(0, lds);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         const int rr = max(0, min(wrow0 + 16 * nb + row, nrows - 1));
-        rq[nb] = p.qids[(size_t)job * p.maxr + rr / p.group];
+        rq[nb] = qb >= 0 ? qb + rr / p.group : p.qids[(size_t)job * p.maxr + rr / p.group];
     }
     u32x4 qf[NB][KS];
 #pragma unroll
@@ -674,6 +692,7 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
 #pragma unroll
         for (int k = 0; k < KS; ++k) qf[nb][k] = *(const u32x4 *)(src + 32 * k);
     }
+    if (qb >= 0 && ntot > 0) copy_tile(0, lds);  // behind the Q loads: one wait covers both
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         const bool valid = wrow0 + 16 * nb + row < nrows;
@@ -683,13 +702,13 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
             asm volatile("" : "+v"(qf[nb][k]));
         }
     }
-    for (int t = 1; t < STAGES - 1 && t < ntot; ++t) copy_tile(t, tile_stage(t));
+    for (int t = 1; t < STAGES && t < ntot; ++t) copy_tile(t, tile_stage(t));
 
     M acc;
     acc.reset();
     const LdsOfs of = T::offsets(row, g4);
 
-    wait_tiles<BPW>(min(ntot, STAGES - 1) - 1);  // tile 0 landed (tiles 1 .. STAGES-2 may be in flight)
+    wait_tiles<BPW>(min(ntot, STAGES) - 1);  // tile 0 landed (tiles 1 .. STAGES-1 may be in flight)
     __builtin_amdgcn_s_barrier();
     if (active && nsteps > 0) {
         f32x4 s0[NB][2];
@@ -700,15 +719,18 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
         if (nsteps > 1) TM::load_k(lds, of, 32, acc.kf);
     }
 
-    // Entering tile t (at step 2t): tile t+1 must have landed, since this
-    // tile's first block reads its K (tiles t+2 .. t+STAGES-2 may still be in
-    // flight); once every wave passed the barrier the stage of tile t-1 is
-    // free for tile t+STAGES-1.
+    // Entering tile t (at step 2t): at the start of a group (t % SYNC == 0)
+    // tiles t+1 .. t+SYNC must have landed (the earlier ones were waited for
+    // at the previous group); tiles up to t+STAGES-SYNC-1 may still be in
+    // flight.  Once every wave passed the barrier the stages of the previous
+    // group are free for tiles up to t+STAGES-1.
     auto sync_tile = [&](int t) {
-        if (t + 1 >= ntot) return;
-        wait_tiles<BPW>(min(t + STAGES - 2, ntot - 1) - (t + 1));
+        if (t % SYNC != 0 || t + 1 >= ntot) return;
+        const int last = t == 0 ? STAGES - 1 : t + STAGES - SYNC - 1;  // last tile issued so far
+        wait_tiles<BPW>(max(0, min(last, ntot - 1) - (t + SYNC)));
         __builtin_amdgcn_s_barrier();
-        if (t + STAGES - 1 < ntot) copy_tile(t + STAGES - 1, tile_stage(t + STAGES - 1));
+        if (t > 0)
+            for (int u = max(t + STAGES - SYNC, t + 1); u < t + STAGES && u < ntot; ++u) copy_tile(u, tile_stage(u));
     };
     // steady state: steps whose successor is neither the last nor masked
     int g = 0;
@@ -739,29 +761,25 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     // Attached segments, in rounds of up to STAGES tiles that are resident
     // together: one wait and one barrier per round, then every wave attends
     // the round's tiles of the segments holding its rows, side by side.  The
-    // root loop already issued the first tiles (up to ntiles + STAGES - 2).
+    // root loop (or the prologue) already issued the first tiles.
     {
-        int issued = min(ntiles + STAGES - 1, ntot);
+        int issued = min((ntiles > 0 ? (ntiles - 1) / SYNC * SYNC : 0) + STAGES, ntot);
         for (int r0 = ntiles; r0 < ntot; r0 += STAGES) {
             const int r1 = min(r0 + STAGES, ntot);
             __builtin_amdgcn_s_barrier();  // every wave is done with the tiles before r0
             for (; issued < r1; ++issued) copy_tile(issued, tile_stage(issued));
             __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
             __builtin_amdgcn_s_barrier();  // the round's tiles landed
-            int u = ntiles;  // sequence index of segment k's first tile
-            for (int k = 0; k < nx && u < r1; ++k) {
-                int xs, xe;
-                seg_span(k, xs, xe);
-                const int n = seg_tiles(xs, xe), xb = xs & ~7;
-                const int rlo = xt[3 + 3 * k] - wrow0;  // segment rows in this wave: [rlo, rlo + group)
-                if (active && rlo >= 0 && rlo < 16 * NB) {
-                    for (int i = max(0, r0 - u); i < n && u + i < r1; ++i) {
-                        const int t0 = xb + i * T::TT;
-                        acc.tail_tile(tile_stage(u + i), qf, of, max(0, xs - t0),
-                                      min(T::TT, xe - t0), rlo, rlo + p.group, row, g4, c, rc);
+#pragma unroll
+            for (int k = 0; k < XM; ++k) {
+                const int rlo = rec[3 + 3 * k] - wrow0;  // segment rows in this wave: [rlo, rlo + group)
+                if (xn[k] > 0 && active && rlo >= 0 && rlo < 16 * NB) {
+                    for (int i = max(0, r0 - xfirst[k]); i < xn[k] && xfirst[k] + i < r1; ++i) {
+                        const int t0 = (xs[k] & ~7) + i * T::TT;
+                        acc.tail_tile(tile_stage(xfirst[k] + i), qf, of, max(0, xs[k] - t0), min(T::TT, xe[k] - t0),
+                                      rlo, rlo + p.group, row, g4, c, rc);
                     }
                 }
-                u += n;
             }
         }
     }

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "tree_attn.h"
+
 namespace ta {
 
 using u16 = unsigned short;
@@ -140,11 +142,15 @@ struct SegParams {
     const int32_t *slots, *counts;
     u16 *out;
     int maxs;
-    // TA_LARGE256 items only (nullable): per item xtail_stride ints -- the
-    // number of attached private segments, then (first token, tokens, first
-    // job row) of each; the item folds them into its rows' partials
+    // TA_LARGE256 items only (nullable): per item xtail_stride (=
+    // TA_XTAIL_STRIDE) ints -- the number of attached private segments (at
+    // most TA_XTAIL_MAX), then (first token, tokens, first job row) of each;
+    // the item folds them into its rows' partials
     const int32_t *xtail;
     int xtail_stride;
+    // nullable: per job the first request id when its requests are
+    // consecutive, else -1 (the TA_LARGE256 kernel then skips the qids lookup)
+    const int32_t *qbase;
 };
 
 // Kernel timing hook (ta_time_next_launch): when set, the next kernel this

@@ -585,7 +585,7 @@ int segment_launch(const void *q, const void *kp, const void *vp, const int32_t 
                    int32_t n_items, int32_t kind, void *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
                    int32_t d, int32_t tcap, int32_t maxr, int32_t dtype, const int32_t *slots,
                    const int32_t *counts, void *out, int32_t maxs, const int32_t *xtail, int32_t xtail_stride,
-                   void *stream) {
+                   const int32_t *qbase, void *stream) {
     if (int e = check_common(hq, hk, d, dtype)) return e;
     if (n_items < 0 || nreq <= 0 || tcap <= 0 || maxr <= 0 || kind < TA_SMALL || kind > TA_TAIL) return TA_ERR_ARG;
     if (n_items == 0) return 0;
@@ -603,7 +603,7 @@ int segment_launch(const void *q, const void *kp, const void *vp, const int32_t 
 #ifdef TA_LEGACY_LARGE
         return TA_ERR_ARG;  // the register-staged kernels take no attached segments
 #endif
-        if (kind != TA_LARGE256 || tcap % 8 != 0 || xtail_stride < 1) return TA_ERR_ARG;
+        if (kind != TA_LARGE256 || tcap % 8 != 0 || xtail_stride != TA_XTAIL_STRIDE) return TA_ERR_ARG;
     }
     SegParams sp;
     sp.q = static_cast<const u16 *>(q);
@@ -630,6 +630,7 @@ int segment_launch(const void *q, const void *kp, const void *vp, const int32_t 
     sp.maxs = maxs;
     sp.xtail = xtail;
     sp.xtail_stride = xtail_stride;
+    sp.qbase = qbase;
     const hipStream_t st = static_cast<hipStream_t>(stream);
 #define TA_SEG(D, F) launch_segment<D, F>(sp, kind, st)
     return (int)TA_DISPATCH(d, dtype == TA_FP16, TA_SEG);
@@ -642,7 +643,7 @@ int plan_segment(const void *q, const void *kp, const void *vp, int32_t tcap, co
     return segment_launch(q, kp, vp, plan->qids, plan->kstart, plan->qlen, plan->klen, plan->rowbase,
                           plan->items[kind], plan->n_items[kind], kind, plan->part, plan->lse, plan->nreq, plan->hq,
                           plan->hk, plan->d, tcap, plan->maxr, plan->dtype, plan->slots, plan->counts, out,
-                          plan->maxs, xt ? plan->xtail : nullptr, xt ? plan->xtail_stride : 0, stream);
+                          plan->maxs, xt ? plan->xtail : nullptr, xt ? plan->xtail_stride : 0, plan->qbase, stream);
 }
 
 }  // namespace
@@ -654,7 +655,7 @@ int ta_segment(const void *q, const void *kp, const void *vp, const int32_t *qid
                int32_t n_items, int32_t kind, void *part, float *lse, int32_t nreq, int32_t hq, int32_t hk,
                int32_t d, int32_t tcap, int32_t maxr, int32_t dtype, void *stream) {
     return segment_launch(q, kp, vp, qids, kstart, qlen, klen, rowbase, items, n_items, kind, part, lse, nreq, hq,
-                          hk, d, tcap, maxr, dtype, nullptr, nullptr, nullptr, 0, nullptr, 0, stream);
+                          hk, d, tcap, maxr, dtype, nullptr, nullptr, nullptr, 0, nullptr, 0, nullptr, stream);
 }
 
 int ta_merge(const void *part, const float *lse, const int32_t *slots, const int32_t *counts, void *out,

@@ -36,7 +36,7 @@ class TaPlan(ctypes.Structure):
         ("part", _c_ptr), ("lse", _c_ptr),
         ("njobs", _c_i32), ("maxr", _c_i32), ("maxs", _c_i32), ("nreq", _c_i32), ("nslot", _c_i32),
         ("hq", _c_i32), ("hk", _c_i32), ("d", _c_i32), ("dtype", _c_i32), ("n_rest", _c_i32),
-        ("xtail", _c_ptr), ("xtail_stride", _c_i32),
+        ("xtail", _c_ptr), ("xtail_stride", _c_i32), ("qbase", _c_ptr),
     ]
 
 

@@ -75,6 +75,7 @@ class PreparedPlan:
     plan: Plan | None = None
     options: dict = field(default_factory=dict)  # prepare's tile_rows / fixed_from
     growing_len: int | None = None  # last CachedDecodePlan.update length of the growing jobs
+    qbase_host: list = field(default_factory=list)  # per job: first request if consecutive, else -1
     _unattached: "PreparedPlan | None" = None
 
     def fill_growing(self, length: int) -> None:
@@ -140,7 +141,7 @@ def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256, tails=frozense
 
 
 TOKEN_QUANTUM = 64  # tokens per LDS tile of the segment kernels
-XTAIL_MAX = 8       # private segments one TA_LARGE256 work item takes on
+XTAIL_MAX = 4       # private segments one TA_LARGE256 work item takes on (TA_XTAIL_MAX, tree_attn.h)
 WAVE_ROWS = 32      # query rows of one wave of the TA_LARGE256 kernel
 
 
@@ -350,15 +351,20 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     if not attached:
         xtail = np.zeros((0, xstride), dtype=np.int32)
 
-    arrays = [qids, kids, qlen, klen, slot_array, counts, rowbase, rest, xtail] + [items[k] for k in sorted(items)]
+    # first request of each job over consecutive requests, else -1 (kernels.py:23-26, 138)
+    qbase = np.array([j.requests[0] if j.requests == tuple(range(j.requests[0], j.requests[0] + len(j.requests)))
+                      else -1 for j in jobs], dtype=np.int32)
+
+    arrays = ([qids, kids, qlen, klen, slot_array, counts, rowbase, rest, xtail, qbase]
+              + [items[k] for k in sorted(items)])
     dev = q.device
     metadata = torch.from_numpy(np.concatenate([a.ravel() for a in arrays])).to(dev)
     views, offset = [], 0
     for array in arrays:
         views.append(metadata[offset:offset + array.size].view(array.shape))
         offset += array.size
-    qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t, rest_t, xtail_t = views[:9]
-    item_views = dict(zip(sorted(items), views[9:]))
+    qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t, rest_t, xtail_t, qbase_t = views[:10]
+    item_views = dict(zip(sorted(items), views[10:]))
     contiguous_q = all(j.requests[-1] - j.requests[0] + 1 == len(j.requests) for j in jobs)
     # partial rows: fp16 scaled by 2^-e per row; lse holds (log-sum-exp, e) per row
     part = torch.empty((nslot, hq, dim), device=dev, dtype=torch.float16)
@@ -380,11 +386,12 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     abi.hq, abi.hk, abi.d = hq, kvheads, dim
     abi.dtype = _DTYPES.get(q.dtype, -1)
     abi.xtail, abi.xtail_stride = (xtail_t.data_ptr(), xstride) if attached else (None, 0)
+    abi.qbase = qbase_t.data_ptr()
     keyed = {(j + small_jobs, row0): segs for (j, row0), segs in attached.items()}
     return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
                         slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t,
                         keyed, xtail_t if attached else None, plan,
-                        {"tile_rows": tile_rows, "fixed_from": fixed_from})
+                        {"tile_rows": tile_rows, "fixed_from": fixed_from}, None, qbase.tolist())
 
 
 def pack_kv(k: torch.Tensor, v: torch.Tensor):
