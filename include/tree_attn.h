@@ -150,6 +150,21 @@ int ta_tail_merge(const void *q, const void *kp, const void *vp,
 int ta_segment_plan(const void *q, const void *kp, const void *vp, int32_t tcap,
                     const ta_plan *plan, int32_t kind, void *stream);
 
+/* One decode step's per-layer glue of the model adapter in one launch
+ * (replaces apply_rotary_pos_emb, the two index_copy_ scatters into the
+ * pools and the Q layout copy of qwen.py:86-91 / kernels.py:157).  For each
+ * request r: q [nreq, hq, d], k and v [nreq, hk, d] (contiguous rows of the
+ * projected, normalised step), cos and sin [d] at cos + r*cs_stride (0 for one
+ * row shared by all requests); Q and K are rotated (rotate-half RoPE, each
+ * multiply and the add rounded to dtype as the eager ops are), Q is written to
+ * q_out [nreq, hq, d], K to kp[h, :, slots[r]] and V to vp[h, slots[r], :]
+ * (pools [hk, d, tcap] / [hk, tcap, d]); a slot outside [0, tcap) writes
+ * nothing.  No counterpart kernel in the reference. */
+int ta_decode_append(const void *q, const void *k, const void *v, const void *cos, const void *sin,
+                     int32_t cs_stride, const int32_t *slots, void *kp, void *vp, void *q_out,
+                     int32_t nreq, int32_t hq, int32_t hk, int32_t d, int32_t tcap, int32_t dtype,
+                     void *stream);
+
 /* Kernel timing hook.  No counterpart in the reference, which times kernels
  * with device events around whole launches (scripts/profile_kernel.py:17-33).
  * The next kernel this library launches on the calling host thread records

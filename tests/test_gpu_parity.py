@@ -15,8 +15,8 @@ import torch
 from oracle.attention_oracle import relative_l2, request_attention
 from tree_attention import CostModel, KVTree, schedule, shapes
 from tree_attention import _native
-from tree_attention.kernels import (CachedDecodePlan, attention, attention_matrix, merge, pack_kv, prepare,
-                                    segment, tail_merge)
+from tree_attention.kernels import (CachedDecodePlan, attention, attention_matrix, decode_append, merge, pack_kv,
+                                    prepare, segment, tail_merge)
 from tree_attention.schedule import Job, Plan
 
 pytestmark = pytest.mark.gpu
@@ -450,3 +450,46 @@ def test_graph_replay_matches_eager(device):
         other = attention_matrix(torch.flip(qd, [0]).contiguous(), kp, vp, prepared).clone()
         torch.cuda.synchronize()
         assert not torch.equal(other, eager)
+
+
+def _rotate_half(x):
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hk,d,shared_rope", [(32, 8, 128, False), (16, 2, 64, True), (8, 8, 32, False)])
+def test_decode_append_matches_eager_ops(hq, hk, d, shared_rope, dtype, device):
+    """The fused decode glue equals the eager RoPE + index_copy_ + contiguous of the adapter
+    (reference qwen.py:86-91) bit for bit; slots outside the pool write nothing."""
+    g = torch.Generator().manual_seed(hq + d)
+    nreq, tcap = 24, 200
+    q = torch.randn(nreq, 1, hq, d, generator=g).to(dtype).to(device)
+    k = torch.randn(nreq, 1, hk, d, generator=g).to(dtype).to(device)
+    v = torch.randn(nreq, 1, hk, d, generator=g).to(dtype).to(device)
+    pos = torch.arange(nreq, dtype=torch.float32)[:, None] * 7 + 3
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    emb = torch.cat([pos * inv, pos * inv], dim=-1)[:, None, :]  # [R, 1, D]
+    if shared_rope:
+        emb = emb[:1]
+    cos, sin = emb.cos().to(dtype).to(device), emb.sin().to(dtype).to(device)
+    slots = torch.randperm(tcap, generator=g)[:nreq].to(torch.int32)
+    slots[0] = tcap - 1
+    slots[1] = tcap + 5  # outside the pool: no write
+    kp0 = torch.randn(hk, d, tcap, generator=g).to(dtype).to(device)
+    vp0 = torch.randn(hk, tcap, d, generator=g).to(dtype).to(device)
+    # eager ops, as the unfused adapter runs them
+    qt, kt = q.transpose(1, 2), k.transpose(1, 2)
+    c, s_ = cos[:, None], sin[:, None]
+    q_ref = (qt * c) + (_rotate_half(qt) * s_)
+    k_ref = (kt * c) + (_rotate_half(kt) * s_)
+    kp_ref, vp_ref = kp0.clone(), vp0.clone()
+    ok = slots < tcap
+    idx = slots[ok].long().to(device)
+    kp_ref.index_copy_(2, idx, k_ref[ok.to(device), :, 0, :].permute(1, 2, 0))
+    vp_ref.index_copy_(1, idx, v.transpose(1, 2)[ok.to(device), :, 0, :].permute(1, 0, 2))
+    kp, vp = kp0.clone(), vp0.clone()
+    out = decode_append(q, k, v, cos, sin, slots.to(device), kp, vp)
+    torch.cuda.synchronize()
+    assert torch.equal(out, q_ref[:, :, 0, :].contiguous())
+    assert torch.equal(kp, kp_ref) and torch.equal(vp, vp_ref)

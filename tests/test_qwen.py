@@ -124,6 +124,28 @@ def test_decode_matches_full_forward_gpu(cached, dtype, device):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_decode_glue_equals_eager_glue(dtype, device):
+    """The fused per-layer glue (RoPE, pool scatters, Q layout in one launch) gives the
+    same logits, bit for bit, as the eager ops of the reference adapter."""
+    model = tiny_model(dtype, device)
+    for cls in (integration.SharedKVDecoder, integration.CachedPrefixDecoder):
+        fused = cls(model, SEQUENCES, 3, "cube", fused_glue=True)
+        eager = cls(model, SEQUENCES, 3, "cube", fused_glue=False)
+        for _ in range(3):
+            tokens = fused.logits.argmax(-1).tolist()
+            a, b = fused.step(tokens), eager.step(tokens)
+            assert torch.equal(a, b)
+        # written pool positions: the prompt tree and each request's generated tail slots
+        written = list(range(fused.prefix_size)) + [fused.prefix_size + r * fused.max_new_tokens + t
+                                                    for r in range(len(SEQUENCES)) for t in range(fused.generated)]
+        idx = torch.tensor(written, device=device)
+        for (kp1, vp1), (kp2, vp2) in zip(fused.pools, eager.pools):
+            assert torch.equal(kp1.index_select(2, idx), kp2.index_select(2, idx))
+            assert torch.equal(vp1.index_select(1, idx), vp2.index_select(1, idx))
+
+
+@pytest.mark.gpu
 def test_per_layer_attention_vs_oracle_gpu(device, monkeypatch):
     """scripts/model_checks.py:42-64: every layer's tree attention vs FP32 on the same Q/K/V."""
     model = tiny_model(torch.bfloat16, device)
@@ -147,25 +169,9 @@ def test_per_layer_attention_vs_oracle_gpu(device, monkeypatch):
 
 
 def qwen3_4b_workload(seed=5):
-    """32 requests: a 2048-token prompt, a 4-way branch of 64-token nodes, 8 suffixes of 128 tokens each.
-
-    Token ids are uniform over Qwen3's 151,936-entry vocabulary.  The branch
-    nodes' length (64) is this workload's own choice; the resulting tree is
-    asserted, since random ids could merge nodes.
-    """
-    g = torch.Generator().manual_seed(seed)
-    ids = lambda n: torch.randint(0, 151_936, (n,), generator=g).tolist()  # noqa: E731
-    prompt = ids(2048)
-    sequences = []
-    for _ in range(4):
-        branch = ids(64)
-        for _ in range(8):
-            sequences.append(prompt + branch + ids(128))
-    tree = KVTree.from_sequences(sequences)
-    lengths = sorted(len(n.tokens) for n in tree.nodes if n.tokens)  # the root node is empty
-    assert lengths == [64] * 4 + [128] * 32 + [2048], "random ids merged nodes of the workload tree"
-    assert tree.storage_tokens == 2048 + 4 * 64 + 32 * 128
-    return sequences
+    """The shared workload builder (tree_attention.shapes), which checks the tree."""
+    from tree_attention import shapes
+    return shapes.qwen3_4b_workload(seed)
 
 
 @pytest.mark.gpu

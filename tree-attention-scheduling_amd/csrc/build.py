@@ -36,6 +36,7 @@ VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 SOURCES = [
     (HERE / "tree_attn.hip", VGPR_FORM),
     (HERE / "segment_tile.hip", VGPR_FORM + ["-fno-honor-nans"]),
+    (HERE / "decode_append.hip", ["-ffp-contract=off"]),  # each RoPE product rounded, as the eager ops
 ]
 
 

@@ -24,7 +24,7 @@ _c_i32 = ctypes.c_int32
 _c_ptr = ctypes.c_void_p
 
 EXPORTS = ("ta_version", "ta_error_string", "ta_segment", "ta_merge", "ta_attention_matrix",
-           "ta_tail_merge", "ta_segment_plan", "ta_time_next_launch")
+           "ta_tail_merge", "ta_segment_plan", "ta_decode_append", "ta_time_next_launch")
 
 
 class TaPlan(ctypes.Structure):
@@ -77,6 +77,9 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         lib.ta_tail_merge.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_i32, ctypes.POINTER(TaPlan), _c_ptr, _c_ptr]
         lib.ta_segment_plan.restype = ctypes.c_int
         lib.ta_segment_plan.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_i32, ctypes.POINTER(TaPlan), _c_i32, _c_ptr]
+        lib.ta_decode_append.restype = ctypes.c_int
+        lib.ta_decode_append.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i32, _c_ptr, _c_ptr, _c_ptr,
+                                         _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_ptr]
         lib.ta_time_next_launch.restype = ctypes.c_int
         lib.ta_time_next_launch.argtypes = [_c_ptr, _c_ptr]
         if path is None:

@@ -1,0 +1,123 @@
+"""Decode-step benchmark of the Qwen3-4B-shaped workload with cached tree-attention plans.
+
+    python -m tree_attention.benchmark_decode [--steps 16] [--layers 36] [--method cube]
+
+Counterpart of the reference's scripts/benchmark_decode_plan.py (a cached
+prompt plan whose tails grow by one token per step, :21-64) and
+scripts/benchmark_qwen.py (the model around it), on one MI355X:
+
+* model: Qwen3-4B-shaped (hidden 2560, 32 query / 8 KV heads, head dim 128,
+  FFN 9728, vocabulary 151,936, RoPE theta 1e6), ``--layers`` layers (36 by
+  default), random-init bf16 weights (no checkpoint is fetched);
+* workload: ``shapes.qwen3_4b_workload`` -- 32 requests over a 2048-token
+  prompt, a 4-way branch of 64-token nodes and 8 suffixes of 128 tokens each;
+* prefill through the model's own attention, then ``--steps`` greedy decode
+  steps of ``CachedPrefixDecoder`` (the prompt is planned once; each step only
+  sets the tails' lengths).
+
+It runs the steps twice on two decoders fed the same tokens: with the fused
+per-layer decode glue (RoPE, the pool scatters and the Q layout in one launch,
+``kernels.decode_append``) and with the eager ops of the reference adapter.
+Per step it reports the wall time (device synchronised on both sides) and the
+per-layer attention time (HIP events around each ``attention_matrix`` call),
+and checks that both decoders produced identical logits.  Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import statistics
+import time
+
+import torch
+
+from . import CostModel, shapes
+from . import qwen as integration
+
+
+def _model(layers: int, device):
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    cfg = Qwen3Config(vocab_size=151_936, hidden_size=2560, intermediate_size=9728, num_hidden_layers=layers,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, rope_theta=1e6,
+                      max_position_embeddings=4096)
+    torch.manual_seed(2027)
+    previous = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(device):
+            return Qwen3ForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(previous)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--steps", type=int, default=16)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--method", default="cube")
+    ap.add_argument("--warmup", type=int, default=2, help="decode steps run before the timed ones")
+    args = ap.parse_args(argv)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    model = _model(args.layers, dev)
+    sequences = shapes.qwen3_4b_workload()
+    budget = args.steps + args.warmup
+    t0 = time.perf_counter()
+    decoders = {name: integration.CachedPrefixDecoder(model, sequences, budget, args.method, CostModel.mi355x(),
+                                                      fused_glue=fused)
+                for name, fused in (("fused", True), ("eager", False))}
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+
+    original = integration.attention_matrix
+    attn_events = []
+
+    def timed_attention(q, kp, vp, prepared):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        out = original(q, kp, vp, prepared)
+        stop.record()
+        attn_events.append((start, stop))
+        return out
+
+    step_ms = {name: [] for name in decoders}
+    attn_us = {name: [] for name in decoders}
+    identical = True
+    integration.attention_matrix = timed_attention
+    try:
+        for step in range(budget):
+            tokens = decoders["fused"].logits.argmax(-1).tolist()
+            logits = {}
+            for name, decoder in decoders.items():
+                attn_events.clear()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                logits[name] = decoder.step(tokens)
+                torch.cuda.synchronize()
+                dt = (time.perf_counter() - t0) * 1e3
+                if step >= args.warmup:
+                    step_ms[name].append(dt)
+                    attn_us[name].append(statistics.mean(a.elapsed_time(b) * 1e3 for a, b in attn_events))
+            identical &= bool(torch.equal(logits["fused"], logits["eager"]))
+    finally:
+        integration.attention_matrix = original
+
+    cached = decoders["fused"].cached_plan.prepared
+    line = {
+        "benchmark": "qwen3_4b_shaped_decode",
+        "config": {"layers": args.layers, "requests": len(sequences), "prompt_tree_tokens": decoders["fused"].prefix_size,
+                   "method": args.method, "cost_model": "mi355x", "steps": args.steps, "warmup": args.warmup,
+                   "dtype": "bf16", "weights": "random-init"},
+        "step_ms": {n: round(statistics.median(v), 3) for n, v in step_ms.items()},
+        "attention_us_per_layer": {n: round(statistics.median(v), 2) for n, v in attn_us.items()},
+        "glue_saving_us_per_layer": round((statistics.median(step_ms["eager"]) - statistics.median(step_ms["fused"]))
+                                          * 1e3 / args.layers, 2),
+        "fused_equals_eager": identical,
+        "plan": {"jobs": len(cached.jobs), "items": list(cached.abi.n_items), "attached": len(cached.attached)},
+        "prefill_s": round(prefill_s, 2),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

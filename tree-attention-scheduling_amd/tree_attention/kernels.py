@@ -496,6 +496,49 @@ def merge(prepared, kp=None):
     return p.out
 
 
+def decode_append(q, k, v, cos, sin, slots, kp, vp, q_out=None):
+    """One decode step's per-layer glue in one HIP launch (``ta_decode_append``).
+
+    Replaces the reference adapter's ``apply_rotary_pos_emb`` (qwen.py:86),
+    the two ``index_copy_`` scatters of the step's K and V into the pools
+    (qwen.py:89-90) and the Q layout copy (qwen.py:91, kernels.py:157):
+    ``q [R, HQ, D]``, ``k, v [R, HK, D]`` (any view that flattens to those
+    rows, e.g. the ``[R, 1, H, D]`` projections), ``cos, sin`` with ``D``
+    values per request (``[R, 1, D]``) or one row for all, ``slots [R]`` the
+    step's pool positions, ``kp [HK, D, T]`` / ``vp [HK, T, D]``.  Returns the
+    rotated Q ``[R, HQ, D]`` (``q_out`` if given).  The results are
+    bit-identical to the eager ops in bf16 and fp16.
+    """
+    nreq = q.shape[0]
+    d = q.shape[-1]
+    q2, k2, v2 = q.reshape(nreq, -1, d), k.reshape(nreq, -1, d), v.reshape(nreq, -1, d)
+    hq, hk = q2.shape[1], k2.shape[1]
+    if q.dtype not in _DTYPES or any(t.dtype != q.dtype for t in (k, v, cos, sin, kp, vp)):
+        raise ValueError("q, k, v, cos, sin and the pools must share dtype bfloat16 or float16")
+    if tuple(v2.shape) != (nreq, hk, d) or kp.shape[:2] != (hk, d) or tuple(vp.shape) != (hk, kp.shape[2], d):
+        raise ValueError("k/v must be [R, HK, D] and the pools [HK, D, T] / [HK, T, D]")
+    if not (kp.is_contiguous() and vp.is_contiguous()):
+        raise ValueError("kp and vp must be contiguous")
+    cos2, sin2 = cos.reshape(-1, d), sin.reshape(-1, d)
+    if cos2.shape != sin2.shape or cos2.shape[0] not in (1, nreq):
+        raise ValueError("cos and sin need D values per request or one row for all")
+    cs_stride = d if cos2.shape[0] == nreq else 0
+    q2, k2, v2, cos2, sin2 = (t.contiguous() for t in (q2, k2, v2, cos2, sin2))
+    slots = slots.to(device=q.device, dtype=torch.int32).contiguous()
+    if slots.numel() != nreq:
+        raise ValueError("slots needs one pool position per request")
+    if q_out is None:
+        q_out = torch.empty((nreq, hq, d), device=q.device, dtype=q.dtype)
+    lib = _native.load()
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.ta_decode_append(q2.data_ptr(), k2.data_ptr(), v2.data_ptr(), cos2.data_ptr(), sin2.data_ptr(),
+                                  cs_stride, slots.data_ptr(), kp.data_ptr(), vp.data_ptr(), q_out.data_ptr(),
+                                  nreq, hq, hk, d, kp.shape[2], _DTYPES[q.dtype], stream)
+    _native.check(rc)
+    return q_out
+
+
 def launch_durations_us(fn, n: int, device=None) -> list:
     """Kernel durations of ``n`` eager calls ``fn(0..n-1)`` on the current stream, in microseconds.
 

@@ -16,7 +16,11 @@ Pool layout (the layout the HIP segment kernels read):
 
 Per decode step each layer's attention forward is swapped for one that writes
 the step's RoPE'd K/V into the pools and calls ``attention_matrix`` on them;
-the original forwards are restored afterwards.  ``attention_matrix`` is looked
+the original forwards are restored afterwards.  The RoPE, the two pool
+scatters and the Q layout copy run as one HIP launch per layer
+(``kernels.decode_append``, bit-identical to the eager ops) for bf16 / fp16
+models on the GPU; ``fused_glue=False`` (and fp32 or CPU models) keep the eager
+ops.  ``attention_matrix`` is looked
 up as this module's global at call time, so a checker may wrap it (the
 reference's scripts/model_checks.py:43,59 does).
 """
@@ -26,7 +30,7 @@ from types import MethodType
 
 import torch
 
-from .kernels import CachedDecodePlan, attention_matrix, prepare
+from .kernels import CachedDecodePlan, attention_matrix, decode_append, prepare
 from .schedule import CostModel, schedule
 from .tree import KVTree
 
@@ -52,13 +56,16 @@ class SharedKVDecoder:
     (reference qwen.py:58-61,74-103).
     """
 
-    def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None):
+    def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None, fused_glue=None):
         self.model = model
         self.sequences = [list(s) for s in sequences]
         self.tree = KVTree.from_sequences(self.sequences)
         self.method = method
         self.cost_model = cost_model or CostModel()
         self.device = next(model.parameters()).device
+        if fused_glue is None:  # the fused launch covers bf16 / fp16 models on the GPU
+            fused_glue = self.device.type == "cuda" and model.dtype in (torch.bfloat16, torch.float16)
+        self.fused_glue = fused_glue
         cfg = model.config
         self.hq = cfg.num_attention_heads
         self.hk = cfg.num_key_value_heads
@@ -130,22 +137,29 @@ class SharedKVDecoder:
         if len(token_ids) != len(self.sequences):
             raise ValueError("step needs exactly one token per request")
         rope_pos = torch.tensor([[len(s)] for s in self.sequences], device=self.device)
-        slots = torch.tensor(self._append(token_ids), device=self.device)
+        slots = torch.tensor(self._append(token_ids), device=self.device, dtype=torch.int32)
         prepared = self._prepare_plan()
         pools = self.pools
         nreq = len(token_ids)
+        fused = self.fused_glue
 
         def forward(module, hidden_states, position_embeddings, attention_mask=None, **kwargs):
             shape = (*hidden_states.shape[:-1], -1, module.head_dim)
-            q = module.q_norm(module.q_proj(hidden_states).view(shape)).transpose(1, 2)
-            k = module.k_norm(module.k_proj(hidden_states).view(shape)).transpose(1, 2)
-            v = module.v_proj(hidden_states).view(shape).transpose(1, 2)
-            q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
+            # projections of this step: [R, 1, heads, D]
+            q = module.q_norm(module.q_proj(hidden_states).view(shape))
+            k = module.k_norm(module.k_proj(hidden_states).view(shape))
+            v = module.v_proj(hidden_states).view(shape)
             kp, vp = pools[module.layer_idx]
-            # q, k, v: [R, heads, 1, D] -> pool slots of this step
-            kp.index_copy_(2, slots, k[:, :, 0, :].permute(1, 2, 0))
-            vp.index_copy_(1, slots, v[:, :, 0, :].permute(1, 0, 2))
-            attn = attention_matrix(q[:, :, 0, :].contiguous(), kp, vp, prepared)
+            if fused:
+                q = decode_append(q, k, v, *position_embeddings, slots, kp, vp)
+            else:
+                q, k = apply_rotary_pos_emb(q.transpose(1, 2), k.transpose(1, 2), *position_embeddings)
+                v = v.transpose(1, 2)
+                # q, k, v: [R, heads, 1, D] -> pool slots of this step
+                kp.index_copy_(2, slots.long(), k[:, :, 0, :].permute(1, 2, 0))
+                vp.index_copy_(1, slots.long(), v[:, :, 0, :].permute(1, 0, 2))
+                q = q[:, :, 0, :].contiguous()
+            attn = attention_matrix(q, kp, vp, prepared)
             return module.o_proj(attn.reshape(nreq, 1, -1)), None
 
         layers = self.model.model.layers
@@ -164,8 +178,8 @@ class SharedKVDecoder:
 class CachedPrefixDecoder(SharedKVDecoder):
     """Plans the prompt tree once; each step only sets the decode-tail lengths (qwen.py:106-124)."""
 
-    def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None):
-        super().__init__(model, sequences, max_new_tokens, method, cost_model)
+    def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None, fused_glue=None):
+        super().__init__(model, sequences, max_new_tokens, method, cost_model, fused_glue)
         prompt_plan = schedule(self.tree, self.hq, self.hk, self.dim, self.method, self.cost_model)
         shape_of_q = torch.empty((len(self.sequences), self.hq, self.dim), device=self.device,
                                  dtype=model.dtype)

@@ -19,6 +19,8 @@ Each function returns the ``(parents, lengths, terminals)`` triple accepted by
   requests duplicating the first two leaf paths (35 requests, 20,480 tokens).
 * ``calibration_grid`` -- shapes used only to fit the MI355X cost model; every
   length is disjoint from the evaluation shapes above.
+* ``qwen3_4b_workload`` -- the token sequences of the Qwen3-4B-shaped decode
+  workload (32 requests over a 2048-token prompt, 4 branches, 8 suffixes each).
 """
 from __future__ import annotations
 
@@ -139,3 +141,26 @@ def calibration_grid():
         parents.append(1 + leaf % 2)
         lengths.append((73, 79, 91)[leaf % 3])
     yield "two_level_r60", (parents, lengths, list(range(3, 63)))
+
+
+def qwen3_4b_workload(seed: int = 5) -> list:
+    """32 requests: a 2048-token prompt, a 4-way branch of 64-token nodes, 8 suffixes of 128 tokens each.
+
+    Token ids are uniform over Qwen3's 151,936-entry vocabulary.  The branch
+    nodes' length (64) is this workload's own choice; the resulting tree is
+    checked (``ValueError`` otherwise), since random ids could merge nodes.
+    """
+    import random
+    rng = random.Random(seed)
+    ids = lambda n: [rng.randrange(151_936) for _ in range(n)]  # noqa: E731
+    prompt = ids(2048)
+    sequences = []
+    for _ in range(4):
+        branch = ids(64)
+        for _ in range(8):
+            sequences.append(prompt + branch + ids(128))
+    t = KVTree.from_sequences(sequences)
+    lengths = sorted(len(n.tokens) for n in t.nodes if n.tokens)  # the root node is empty
+    if lengths != [64] * 4 + [128] * 32 + [2048] or t.storage_tokens != 2048 + 4 * 64 + 32 * 128:
+        raise ValueError("random ids merged nodes of the workload tree")
+    return sequences
