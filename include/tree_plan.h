@@ -1,0 +1,56 @@
+/*
+ * tree_plan.h -- C ABI of the host-side grouped planner (libtree_plan.so).
+ *
+ * Replaces the grouped branch of the reference's schedule()
+ * (src/tree_attention/schedule.py:94-151: greedy :103-112, subset DP :113-131)
+ * with its cost model (:41-52).  Host code only; no GPU, no allocation visible
+ * to the caller, no state kept between calls.
+ *
+ * The caller passes the tree in CSR form and receives one decision per node;
+ * materialising the jobs (split() of every node's remaining requests over its
+ * token chain, schedule.py:133-151) stays with the caller, whose plans are then
+ * bit-exact with the reference planner's: same jobs, same order, same
+ * estimated cost.  Valid when the cost is the reference's formula and every
+ * root-to-node id chain is strictly increasing (then a kv_split chunk is one
+ * physical job per consecutive run, schedule.py:13-26); other trees go
+ * through the Python planner.
+ */
+#ifndef TREE_PLAN_H
+#define TREE_PLAN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TP_GREEDY 0
+#define TP_CUBE 1
+
+/*
+ * n nodes, node 0 the root; parent[v] (-1 for the root).
+ * Children of v, in the tree's child order: child_idx[child_off[v] .. child_off[v+1]).
+ * nreq[v]: number of requests whose path passes through v.
+ * Node v's token ids as maximal runs of consecutive ids:
+ *   (run_start[i], run_len[i]) for i in [run_off[v], run_off[v+1]).
+ * fparams: bandwidth (bytes/us), cube_flops (FLOP/us), task_us, merge_us.
+ * iparams: cube_rows, key_tile, kv_split, max_query_rows, qheads, kvheads, dim.
+ * Outputs: pushed[v] = 1 if, in the plan, v's parent hands v its token chain
+ * (SplitQ: v's requests leave the parent's job and attend parent + v tokens
+ * together), else 0 (pushed[0] = 0); total[0] = the DP's cost estimate of the
+ * root state (for greedy, the sum the reference's greedy pass computes).
+ * Returns 0, or 1 for invalid arguments: a table that is not a tree rooted
+ * at 0 with every child numbered after its parent, a child with more
+ * requests below it than its parent holds, an empty run, or unusable model
+ * parameters (qheads % kvheads != 0, nonpositive tile sizes).
+ */
+int tp_grouped_plan(int32_t method, int32_t n, const int32_t *parent, const int32_t *child_off,
+                    const int32_t *child_idx, const int32_t *nreq, const int64_t *run_off,
+                    const int64_t *run_start, const int64_t *run_len, const double *fparams,
+                    const int64_t *iparams, int8_t *pushed, double *total);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TREE_PLAN_H */

@@ -17,6 +17,8 @@ from tree_attention.schedule import Plan, physical_jobs
 
 GOLDEN = Path(__file__).parent / "golden"
 METHODS = ("request", "fixed", "greedy", "cube")
+# greedy / cube decisions: the C++ planner (libtree_plan.so) and the Python one
+IMPLS = pytest.mark.parametrize("native", [True, False], ids=["cpp", "python"])
 
 
 def _load(name):
@@ -33,7 +35,8 @@ def _runs(tokens):
     return out
 
 
-def test_reference_grid_costs_bit_exact():
+@IMPLS
+def test_reference_grid_costs_bit_exact(native):
     """results/tree_grid_run{1,2,3}.json: 81 trees x 4 methods, default CostModel."""
     rows = _load("planner_tree_grid.json")["rows"]
     i = 0
@@ -43,7 +46,7 @@ def test_reference_grid_costs_bit_exact():
             row = rows[i]
             i += 1
             assert row["shape"] == params and row["method"] == method
-            plan = schedule(tree, method=method)
+            plan = schedule(tree, method=method, native=native and method in ("greedy", "cube"))
             plan.validate(tree)
             assert plan.estimated_us == row["estimated_us"], (params, method)
             assert len(plan.jobs) == row["logical_jobs"]
@@ -52,11 +55,12 @@ def test_reference_grid_costs_bit_exact():
     assert i == 324
 
 
-def test_tree_scan_costs_and_choices():
+@IMPLS
+def test_tree_scan_costs_and_choices(native):
     """results/tree_scan.json: 81 small trees, costs, job counts, whether cube differs."""
     for row in _load("planner_tree_scan.json")["rows"]:
         tree = KVTree.synthetic([-1, 0, 0, 1, 1, 2, 2], row["lengths"], [3, 4, 5, 6])
-        plans = {m: schedule(tree, method=m) for m in METHODS}
+        plans = {m: schedule(tree, method=m, native=native and m in ("greedy", "cube")) for m in METHODS}
         norm = {m: sorted((j.requests, j.tokens) for j in p.jobs) for m, p in plans.items()}
         for m, p in plans.items():
             assert p.estimated_us == row["cost_us"][m], (row["lengths"], m)
@@ -91,7 +95,8 @@ def test_npu_correctness_logical_jobs():
         assert len(plan.jobs) == row["logical_jobs"], row
 
 
-def test_plans_match_reference_implementation():
+@IMPLS
+def test_plans_match_reference_implementation(native):
     """Exact job tuples, job order and estimated_us, including non-default parameters."""
     data = _load("plan_fixtures.json")
     n = 0
@@ -100,7 +105,8 @@ def test_plans_match_reference_implementation():
                 else KVTree.synthetic(*case["spec"]))
         for want in case["plans"]:
             q, k, d = want["heads"]
-            plan = schedule(tree, q, k, d, want["method"], CostModel(**want["model"]))
+            grouped = want["method"] in ("greedy", "cube")
+            plan = schedule(tree, q, k, d, want["method"], CostModel(**want["model"]), native=native and grouped)
             got = [[list(j.requests), _runs(j.tokens)] for j in plan.jobs]
             if "jobs" in want:
                 assert got == want["jobs"], (case["name"], want["method"], want["model"])

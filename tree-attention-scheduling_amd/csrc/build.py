@@ -1,4 +1,5 @@
-"""Build ``libtree_attn.so`` (gfx950) next to the ``tree_attention`` package.
+"""Build ``libtree_attn.so`` (gfx950) and ``libtree_plan.so`` (host planner)
+next to the ``tree_attention`` package.
 
     python tree-attention-scheduling_amd/csrc/build.py
 
@@ -18,6 +19,10 @@ HERE = Path(__file__).resolve().parent
 PKG = HERE.parent / "tree_attention"
 INCLUDE = HERE.parent.parent / "include"
 LIB = PKG / "libtree_attn.so"
+PLAN_LIB = PKG / "libtree_plan.so"
+# The planner's costs must round exactly like the Python planner's: no FMA
+# contraction, no fast-math reassociation.
+PLAN_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math", "-Wall"]
 
 COMMON = [
     "-O3", "-std=c++20", "--offload-arch=gfx950", "-fPIC",
@@ -52,7 +57,7 @@ def _run(cmd, verbose):
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+        raise RuntimeError(f"{Path(cmd[0]).name} failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
     if verbose and res.stderr.strip():
         print(res.stderr, file=sys.stderr)
 
@@ -73,6 +78,18 @@ def build(verbose: bool = False, out: Path | None = None, defines=()) -> Path:
     return target
 
 
+def build_planner(verbose: bool = False, out: Path | None = None) -> Path:
+    """Compile the host planner (planner.cpp) into ``out`` (default: in-tree) with g++."""
+    target = Path(out) if out is not None else PLAN_LIB
+    tmp = target.with_name(target.name + f".tmp{os.getpid()}")
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("g++ not found; it is required to build the planner library")
+    _run([cxx, *PLAN_FLAGS, f"-I{INCLUDE}", str(HERE / "planner.cpp"), "-o", str(tmp)], verbose)
+    os.replace(tmp, target)
+    return target
+
+
 if __name__ == "__main__":
     args = sys.argv[1:]
     out = None
@@ -84,3 +101,5 @@ if __name__ == "__main__":
         elif a.startswith("-D"):
             defines.append(a[2:])
     print(build(verbose=True, out=out, defines=defines))
+    if out is None:
+        print(build_planner(verbose=True))

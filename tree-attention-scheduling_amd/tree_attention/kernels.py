@@ -34,6 +34,7 @@ import torch
 
 from . import _native
 from .schedule import Job, Plan, physical_jobs
+from .tree import id_run
 
 _DTYPES = {torch.bfloat16: _native.TA_BF16, torch.float16: _native.TA_FP16}
 SMALL_ROWS = 16  # rows of one MFMA block; same threshold as kernels.py:109-110
@@ -167,39 +168,52 @@ def _attach_tails(small, large, group, tile_rows, is_fixed):
 
     Returns the small jobs left and ``{(large job index, first row): [(job, first job row)]}``.
     """
+    # the 256-row work items: their key (large job index, first row) and the
+    # tiles their own job streams; holders[r]: (job, item, wave, first job row)
+    # of every item whose rows include request r's within one wave
+    keys, own = [], []
     holders = {}
     for J, job in enumerate(large):
         rows = len(job.requests) * group
         if _large_kind(rows, tile_rows) != _native.TA_LARGE256:
             continue
+        first, n = len(keys), _tiles(job)
+        for row0 in range(0, rows, 256):
+            keys.append((J, row0))
+            own.append(n)
         for pos, r in enumerate(job.requests):
-            holders.setdefault(r, []).append((J, pos * group))
-    attached, item_tiles, wave_tiles = {}, {}, {}
+            lrow = pos * group
+            if lrow % WAVE_ROWS + group <= WAVE_ROWS:
+                holders.setdefault(r, []).append((J, first + lrow // 256, lrow % 256 // WAVE_ROWS, lrow))
+    if not holders:
+        return small, {}
+    waves = 256 // WAVE_ROWS
+    item_tiles, item_segs, wave_tiles = [0] * len(keys), [0] * len(keys), [0] * (len(keys) * waves)
+    attached = {}
     left = []
     for job in small:
         r = job.requests[0]
-        if len(job.requests) != 1 or is_fixed(job) or r not in holders:
+        cands = holders.get(r) if len(job.requests) == 1 else None
+        if not cands or is_fixed(job):
             left.append(job)
             continue
         n = _tiles(job)
         best = None
-        for J, lrow in holders[r]:
-            if lrow % WAVE_ROWS + group > WAVE_ROWS:
-                continue  # the request's rows must lie in one wave
-            key = (J, lrow // 256 * 256)
-            wave = (lrow - key[1]) // WAVE_ROWS
-            if len(attached.get(key, ())) >= XTAIL_MAX or item_tiles.get(key, 0) + n > _tiles(large[J]):
+        for J, item, wave, lrow in cands:
+            t = item_tiles[item]
+            if item_segs[item] >= XTAIL_MAX or t + n > own[item]:
                 continue
-            score = (item_tiles.get(key, 0), wave_tiles.get(key + (wave,), 0), J)
+            score = (t, wave_tiles[item * waves + wave], J)
             if best is None or score < best[0]:
-                best = (score, key, wave, lrow)
+                best = (score, item, wave, lrow)
         if best is None:
             left.append(job)
             continue
-        _, key, wave, lrow = best
-        attached.setdefault(key, []).append((job, lrow))
-        item_tiles[key] = item_tiles.get(key, 0) + n
-        wave_tiles[key + (wave,)] = wave_tiles.get(key + (wave,), 0) + n
+        _, item, wave, lrow = best
+        attached.setdefault(keys[item], []).append((job, lrow))
+        item_tiles[item] += n
+        item_segs[item] += 1
+        wave_tiles[item * waves + wave] += n
     return left, attached
 
 
@@ -234,12 +248,12 @@ def _recut(jobs, items_per_chunk, target_items, is_fixed):
     out = []
     for reqs, t0, n, fixed in runs:
         if fixed:
-            out.append(Job(reqs, tuple(range(t0, t0 + n))))
+            out.append(Job(reqs, id_run(t0, t0 + n)))
             continue
         pieces = -(-n // limit)
         size = -(-(-(-n // pieces)) // 8) * 8  # near-equal, 8-token aligned
         for a in range(0, n, size):
-            out.append(Job(reqs, tuple(range(t0 + a, t0 + min(n, a + size)))))
+            out.append(Job(reqs, id_run(t0 + a, t0 + min(n, a + size))))
     return out
 
 
@@ -278,7 +292,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
         toks = job.tokens
         if not job.requests or not toks:
             raise ValueError("Every job needs requests and tokens")
-        if toks[0] < 0 or (len(toks) > 1 and toks != tuple(range(toks[0], toks[0] + len(toks)))):
+        if toks[0] < 0 or (len(toks) > 1 and toks != id_run(toks[0], toks[0] + len(toks))):
             raise ValueError(f"Job {i} tokens are not one run of consecutive physical ids")
     if not jobs:
         raise ValueError("Plan has no jobs")
@@ -352,7 +366,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
         xtail = np.zeros((0, xstride), dtype=np.int32)
 
     # first request of each job over consecutive requests, else -1 (kernels.py:23-26, 138)
-    qbase = np.array([j.requests[0] if j.requests == tuple(range(j.requests[0], j.requests[0] + len(j.requests)))
+    qbase = np.array([j.requests[0] if j.requests == id_run(j.requests[0], j.requests[0] + len(j.requests))
                       else -1 for j in jobs], dtype=np.int32)
 
     arrays = ([qids, kids, qlen, klen, slot_array, counts, rowbase, rest, xtail, qbase]
@@ -569,8 +583,7 @@ class CachedDecodePlan:
     """A prompt schedule plus one contiguous growing KV tail per request (kernels.py:171-186)."""
 
     def __init__(self, prefix_plan, q, prefix_tokens, max_new_tokens):
-        tails = [Job((r,), tuple(range(prefix_tokens + r * max_new_tokens,
-                                       prefix_tokens + (r + 1) * max_new_tokens)))
+        tails = [Job((r,), id_run(prefix_tokens + r * max_new_tokens, prefix_tokens + (r + 1) * max_new_tokens))
                  for r in range(q.shape[0])]
         plan = Plan(prefix_plan.jobs + tails, prefix_plan.method, prefix_plan.estimated_us,
                     prefix_plan.settings)

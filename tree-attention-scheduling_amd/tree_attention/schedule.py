@@ -31,9 +31,10 @@ in the reference).
 from __future__ import annotations
 
 from dataclasses import asdict, dataclass
+from itertools import chain
 from math import ceil
 
-from .tree import KVTree
+from .tree import KVTree, id_run
 
 
 @dataclass(frozen=True)
@@ -130,8 +131,7 @@ class Plan:
 
 def _is_range(toks) -> bool:
     """True if ``toks`` is exactly ``range(toks[0], toks[0] + len(toks))`` (C-speed compare)."""
-    return bool(toks) and toks[-1] - toks[0] + 1 == len(toks) and toks == tuple(
-        range(toks[0], toks[0] + len(toks)))
+    return bool(toks) and toks[-1] - toks[0] + 1 == len(toks) and toks == id_run(toks[0], toks[0] + len(toks))
 
 
 def _runs_of(tokens) -> tuple:
@@ -153,35 +153,44 @@ def _join_runs(a: tuple, b: tuple) -> tuple:
     return a + b
 
 
-def _increasing(tree: KVTree) -> bool:
+def _increasing(tree: KVTree, node_runs=None) -> bool:
     """True if every root-to-node id chain is strictly increasing.
 
     Under that condition a chunk passes the reference's span test
     (``last - first + 1 == len``) exactly when it is one consecutive run, so
-    run-length costs equal the reference's per-job costs.
+    run-length costs equal the reference's per-job costs.  ``node_runs``
+    (each node's ``_runs_of``) saves rescanning the tokens.
     """
-    for node in tree.nodes:
+    nodes = tree.nodes
+    for v, node in enumerate(nodes):
         toks = node.tokens
-        if not _is_range(toks):
-            for i in range(1, len(toks)):
-                if toks[i] <= toks[i - 1]:
-                    return False
+        runs = node_runs[v] if node_runs is not None else _runs_of(toks)
+        for i in range(1, len(runs)):
+            if runs[i][0] <= runs[i - 1][0] + runs[i - 1][1] - 1:
+                return False
         if toks and node.parent >= 0:
             # nearest ancestor with tokens must end below this node's first id
             p = node.parent
-            while p >= 0 and not tree.nodes[p].tokens:
-                p = tree.nodes[p].parent
-            if p >= 0 and tree.nodes[p].tokens[-1] >= toks[0]:
+            while p >= 0 and not nodes[p].tokens:
+                p = nodes[p].parent
+            if p >= 0 and nodes[p].tokens[-1] >= toks[0]:
                 return False
     return True
 
 
-def schedule(tree: KVTree, qheads=32, kvheads=8, dim=128, method="cube", model=None) -> Plan:
+def schedule(tree: KVTree, qheads=32, kvheads=8, dim=128, method="cube", model=None, native=None) -> Plan:
     """Plan one decode step's attention over ``tree`` (reference schedule.py:72-151).
 
     Methods: ``request`` (each request alone), ``fixed`` (one group per tree
     node), ``greedy`` (per-child SplitQ/SplitK choice) and ``cube`` (subset DP
     over children with full descendant cost).
+
+    ``native`` selects the implementation of the greedy / cube decisions:
+    ``None`` uses the C++ planner (libtree_plan.so) when it is built and the
+    case is one it covers (the reference's cost formula, increasing id chains),
+    else this module's; ``True`` requires the C++ planner (``ValueError`` for
+    a case it does not cover); ``False`` uses this module's.  Both give the
+    same plan, bit for bit.
     """
     if qheads % kvheads:
         raise ValueError("Query heads must be divisible by KV heads")
@@ -207,7 +216,7 @@ def schedule(tree: KVTree, qheads=32, kvheads=8, dim=128, method="cube", model=N
     elif method == "fixed":
         jobs = [j for n in nodes for j in split(n.requests, n.tokens)]
     elif method in ("greedy", "cube"):
-        jobs = _grouped_jobs(tree, method, model, split, plan_cost, qheads, kvheads, dim, req_tile)
+        jobs = _grouped_jobs(tree, method, model, split, plan_cost, qheads, kvheads, dim, req_tile, native)
     else:
         raise ValueError(f"Unknown scheduling method: {method}")
     settings = asdict(model)
@@ -215,11 +224,29 @@ def schedule(tree: KVTree, qheads=32, kvheads=8, dim=128, method="cube", model=N
     return Plan(jobs, method, plan_cost(jobs), settings)
 
 
-def _grouped_jobs(tree, method, model, split, plan_cost, qheads, kvheads, dim, req_tile):
+def _native_covers(model) -> bool:
+    """The C++ planner evaluates the cost formula on int64 sizes and double rates."""
+    ints = (model.cube_rows, model.key_tile, model.kv_split, model.max_query_rows)
+    rates = (model.bandwidth, model.cube_flops, model.task_us, model.merge_us)
+    return (type(model)._cost_n is CostModel._cost_n
+            and all(type(x) is int and 0 < x < 2 ** 31 for x in ints)
+            and all(type(x) in (int, float) for x in rates))
+
+
+def _grouped_jobs(tree, method, model, split, plan_cost, qheads, kvheads, dim, req_tile, native=None):
     """Greedy / subset-DP grouping, then pre-order materialisation of jobs."""
     nodes = tree.nodes
     kv_split = model.kv_split
-    fast = type(model).cost is CostModel.cost and _increasing(tree)
+    all_runs = [_runs_of(nd.tokens) for nd in nodes] if type(model).cost is CostModel.cost else None
+    fast = all_runs is not None and _increasing(tree, all_runs)
+    if native is not False:
+        from . import _planner
+        covered = fast and _native_covers(model)
+        if native and not covered:
+            raise ValueError("the C++ planner covers the reference cost formula over increasing id chains only")
+        if covered and (native or _planner.available()):
+            pushed, _ = _planner.grouped_decisions(tree, method, model, qheads, kvheads, dim, all_runs)
+            return _materialise(nodes, split, lambda v, top: {c for c in nodes[v].children if pushed[c]})
 
     # --- token chains ------------------------------------------------------
     # A DP state (v, top) means: node v plus the inherited tokens of the chain
@@ -230,7 +257,7 @@ def _grouped_jobs(tree, method, model, split, plan_cost, qheads, kvheads, dim, r
     def own_runs(v):
         got = node_runs.get(v)
         if got is None:
-            got = node_runs[v] = _runs_of(nodes[v].tokens)
+            got = node_runs[v] = all_runs[v] if all_runs is not None else _runs_of(nodes[v].tokens)
         return got
 
     def runs(v, top):
@@ -259,7 +286,7 @@ def _grouped_jobs(tree, method, model, split, plan_cost, qheads, kvheads, dim, r
             if top is None or u == top:
                 break
             u = nodes[u].parent
-        return tuple(t for part in reversed(parts) for t in part)
+        return parts[0] if len(parts) == 1 else tuple(chain.from_iterable(reversed(parts)))
 
     # --- cost of split(range(count), tokens) -------------------------------
     count_memo = {}
@@ -343,17 +370,35 @@ def _grouped_jobs(tree, method, model, split, plan_cost, qheads, kvheads, dim, r
         memo[key] = evaluate(key)
         stack.pop()
 
-    # --- materialise in pre-order -------------------------------------------
+    return _materialise(nodes, split, lambda v, top: memo[(v, top)][1])
+
+
+def _materialise(nodes, split, pushed_of):
+    """Jobs of the chosen states in pre-order (reference schedule.py:133-151).
+
+    ``pushed_of(v, top)`` is the set of children that state (v, top) pushes;
+    a pushed child's state inherits the chain top -> v.
+    """
+    def chain_tokens(v, top):
+        parts = []
+        u = v
+        while True:
+            parts.append(nodes[u].tokens)
+            if top is None or u == top:
+                break
+            u = nodes[u].parent
+        return parts[0] if len(parts) == 1 else tuple(chain.from_iterable(reversed(parts)))
+
     jobs = []
     todo = [(0, None)]
     while todo:
         v, top = todo.pop()
         node = nodes[v]
-        pushed = memo[(v, top)][1]
+        pushed = pushed_of(v, top)
         detached = {r for c in pushed for r in nodes[c].requests}
         remaining = tuple(r for r in node.requests if r not in detached)
         jobs.extend(split(remaining, chain_tokens(v, top)))
-        ct = child_top(v, top)
+        ct = v if top is None else top
         for c in reversed(node.children):
             todo.append((c, ct if c in pushed else None))
     return jobs

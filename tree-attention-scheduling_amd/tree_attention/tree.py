@@ -15,6 +15,25 @@ from __future__ import annotations
 
 from dataclasses import dataclass, field
 
+_IDS: tuple = ()
+_IDS_MAX = 1 << 20
+
+
+def id_run(start: int, stop: int) -> tuple:
+    """``tuple(range(start, stop))``, sliced from one shared tuple of ids below 2**20.
+
+    Slicing allocates no int objects, and tuples cut from the shared one hold
+    the same objects, so comparing two of them is an identity check per
+    element.  Token ids are compared and re-cut on every plan, which makes
+    this the cheap way to build them.
+    """
+    global _IDS
+    if start < 0 or stop > _IDS_MAX:
+        return tuple(range(start, stop))
+    if stop > len(_IDS):
+        _IDS = tuple(range(min(_IDS_MAX, max(stop, 2 * len(_IDS), 1 << 14))))
+    return _IDS[start:stop]
+
 
 @dataclass
 class Node:
@@ -75,7 +94,7 @@ class KVTree:
             while end < limit and all(seqs[r][end] == lead[end] for r in group):
                 end += 1
             first = len(token_ids)
-            ids = tuple(range(first, first + end - offset))
+            ids = id_run(first, first + end - offset)
             token_ids.extend(lead[offset:end])
             node_id = len(nodes)
             nodes.append(Node(parent, ids, requests=tuple(group)))
@@ -100,7 +119,7 @@ class KVTree:
             valid = parent == -1 if i == 0 else 0 <= parent < i
             if not valid:
                 raise ValueError("Parents must precede children")
-            nodes.append(Node(parent, tuple(range(base, base + length))))
+            nodes.append(Node(parent, id_run(base, base + length)))
             base += length
             if parent >= 0:
                 nodes[parent].children.append(i)
