@@ -102,6 +102,93 @@ def test_pool_layout_and_capacity_cpu(monkeypatch):
         cached.step([1, 1, 1, 1])
 
 
+# prompts with duplicates, a prompt that is a prefix of others and nested branches
+TREE_SEQUENCES = SEQUENCES + [[1, 2, 9], [1, 2, 3, 4, 5, 6, 7], [7, 8], [1, 2, 3, 4, 5, 6, 7, 13, 14]]
+
+
+def test_tree_prefill_matches_request_prefill_cpu():
+    """Shared-prefix prefill (every tree node once) gives the pools and last-token logits of the
+    reference's one-forward-per-request prefill (qwen.py:34-51), up to fp32 reduction order."""
+    model = tiny_model(torch.float32, "cpu")
+    a = integration.SharedKVDecoder(model, TREE_SEQUENCES, 2, "cube", prefill="request")
+    b = integration.SharedKVDecoder(model, TREE_SEQUENCES, 2, "cube", prefill="tree")
+    torch.testing.assert_close(b.logits, full_forward_logits(model, TREE_SEQUENCES, "cpu"), atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(b.logits, a.logits, atol=1e-5, rtol=1e-5)
+    n = a.prefix_size
+    for (ka, va), (kb, vb) in zip(a.pools, b.pools):
+        torch.testing.assert_close(kb[..., :n], ka[..., :n], atol=1e-5, rtol=1e-5)
+        torch.testing.assert_close(vb[:, :n], va[:, :n], atol=1e-5, rtol=1e-5)
+    with pytest.raises(ValueError, match="prefill"):
+        integration.SharedKVDecoder(model, SEQUENCES, 2, "cube", prefill="batch")
+
+
+# four childless siblings of lengths 1-3 under one node, next to inner nodes and a lone leaf
+BRANCHY = [[5, 6, 1], [5, 6, 2, 3], [5, 6, 4, 4, 4], [5, 6, 7], [5, 9, 9], [8], [5, 6, 2, 3]]
+
+
+@pytest.mark.parametrize("leaf_batch", [1, 3, 16])
+def test_tree_prefill_forwards_cpu(leaf_batch, monkeypatch):
+    """Each stored prompt token goes through the model once: inner nodes one forward each,
+    childless siblings right-padded in groups of ``leaf_batch``; logits and pools equal
+    the per-request prefill's (the reference's: every prompt in full)."""
+    model = tiny_model(torch.float32, "cpu")
+    shapes_seen = []
+    forward = model.forward
+
+    def counting(*args, **kwargs):
+        shapes_seen.append(tuple(kwargs["input_ids"].shape))
+        return forward(*args, **kwargs)
+
+    monkeypatch.setattr(integration.SharedKVDecoder, "_prefill",
+                        lambda self: integration.SharedKVDecoder._prefill_tree(self, leaf_batch))
+    monkeypatch.setattr(model, "forward", counting)
+    decoder = integration.SharedKVDecoder(model, BRANCHY, 2, "cube", prefill="request")
+    nodes = decoder.tree.nodes
+    expected = [(1, len(n.tokens)) for n in nodes if n.tokens and n.children]
+    for n in nodes:
+        leaves = [len(nodes[c].tokens) for c in n.children if not nodes[c].children]
+        for i in range(0, len(leaves), leaf_batch):
+            group = leaves[i:i + leaf_batch]
+            expected.append((len(group), max(group)))
+    assert sorted(shapes_seen) == sorted(expected)
+    assert sum(len(n.tokens) for n in nodes) == decoder.prefix_size
+    monkeypatch.undo()
+    reference = integration.SharedKVDecoder(model, BRANCHY, 2, "cube", prefill="request")
+    torch.testing.assert_close(decoder.logits, reference.logits, atol=1e-5, rtol=1e-5)
+    n = decoder.prefix_size
+    for (ka, va), (kb, vb) in zip(reference.pools, decoder.pools):
+        torch.testing.assert_close(kb[..., :n], ka[..., :n], atol=1e-5, rtol=1e-5)
+        torch.testing.assert_close(vb[:, :n], va[:, :n], atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("cached", [False, True])
+def test_tree_prefill_decode_matches_full_forward_cpu(cached, monkeypatch):
+    model = tiny_model(torch.float32, "cpu")
+    cls = integration.CachedPrefixDecoder if cached else integration.SharedKVDecoder
+    decoder = cls(model, TREE_SEQUENCES, 3, "cube", prefill="tree")
+    monkeypatch.setattr(integration, "attention_matrix", OracleAttention(decoder))
+    for step in range(3):
+        actual = decoder.step(decoder.logits.argmax(-1).tolist())
+        reference = full_forward_logits(model, decoder.sequences, "cpu")
+        torch.testing.assert_close(actual, reference, atol=1e-4, rtol=1e-4, msg=lambda m: f"step {step}: {m}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_tree_prefill_decode_gpu(dtype, device):
+    """Tree prefill on the GPU, then 3 greedy steps of the cached plan on the HIP kernels: logits
+    against a full forward at the tolerances of the decode check below."""
+    model = tiny_model(dtype, device)
+    atol, rtol = (0.004, 0.02) if dtype == torch.float16 else (0.016, 0.02)
+    decoder = integration.CachedPrefixDecoder(model, TREE_SEQUENCES, 3, "cube", prefill="tree")
+    torch.testing.assert_close(decoder.logits, full_forward_logits(model, TREE_SEQUENCES, device), atol=atol,
+                               rtol=rtol)
+    for step in range(3):
+        actual = decoder.step(decoder.logits.argmax(-1).tolist())
+        reference = full_forward_logits(model, decoder.sequences, device)
+        torch.testing.assert_close(actual, reference, atol=atol, rtol=rtol, msg=lambda m: f"step {step}: {m}")
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("cached", [False, True])

@@ -583,12 +583,16 @@ struct PipeMath {
 #ifndef TA_PIPE_STAGES
 #define TA_PIPE_STAGES 5
 #endif
+#ifndef TA_PIPE_PRO
+#define TA_PIPE_PRO 3  // measured: 3 of 5 tiles in the prologue start the loop earliest
+#endif
 
 // STAGES LDS tiles; the waves meet at a barrier every SYNC tiles.  While the
 // waves work on tiles t .. t+SYNC-1 they read those and the K of tile t+SYNC
 // (the pipelined steps read one step ahead), so SYNC+1 tiles are resident
-// and STAGES-SYNC-1 more can be in flight.
-template <int D, bool FP16, int NW, int NB = 2, int STAGES = TA_PIPE_STAGES, int SYNC = 1>
+// and STAGES-SYNC-1 more can be in flight.  The prologue issues PRO tiles;
+// the first loop barrier issues the rest of the ring.
+template <int D, bool FP16, int NW, int NB = 2, int STAGES = TA_PIPE_STAGES, int SYNC = 1, int PRO = TA_PIPE_PRO>
 __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     using T = Tile<D>;
     using M = PipeMath<D, FP16, NW, NB>;
@@ -598,6 +602,7 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     static_assert(T::NBLK % NW == 0, "every wave copies the same number of blocks");
     static_assert(SYNC >= 1 && STAGES >= 2 * SYNC + 1 && STAGES <= 5,
                   "a group's tiles, the next K and the next group's copies fit the stages");
+    static_assert(PRO >= SYNC + 1 && PRO <= STAGES, "the prologue issues the tiles the first group reads");
     __shared__ __attribute__((aligned(16))) u16 lds[STAGES * T::ELEMS];
 
     const int total = gridDim.x;
@@ -666,6 +671,8 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
         TM::copy(st, p.kp, p.vp, h, p.tcap, t0n, cs, ce, wave, lane);
     };
 
+    int issued = 0;  // tiles of the sequence whose copies this wave has issued
+
     // Prologue.  Loads retire in order, and a wait for a load's result also
     // waits for every copy issued before it, so the dependent chain
     // (request ids -> Q rows) is kept short.  A job over consecutive requests
@@ -675,7 +682,7 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     // tile 0's copies.  Otherwise tile 0's copies go out with the request-id
     // loads (both are needed before the first step), then the Q loads.  Every
     // lane loads a valid row (rows past the job are zeroed afterwards); tiles
-    // 1 .. STAGES-1 follow once Q has landed.
+    // 1 .. PRO-1 follow.
     const int qb = p.qbase ? p.qbase[job] : -1;
     int rq[NB];
     if (qb < 0 && ntot > 0) copy_tile(0, lds);
@@ -702,13 +709,14 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
             asm volatile("" : "+v"(qf[nb][k]));
         }
     }
-    for (int t = 1; t < STAGES && t < ntot; ++t) copy_tile(t, tile_stage(t));
+    for (int t = 1; t < PRO && t < ntot; ++t) copy_tile(t, tile_stage(t));
+    issued = min(PRO, ntot);
 
     M acc;
     acc.reset();
     const LdsOfs of = T::offsets(row, g4);
 
-    wait_tiles<BPW>(min(ntot, STAGES) - 1);  // tile 0 landed (tiles 1 .. STAGES-1 may be in flight)
+    wait_tiles<BPW>(issued - 1);  // tile 0 landed (tiles 1 .. PRO-1 may be in flight)
     __builtin_amdgcn_s_barrier();
     if (active && nsteps > 0) {
         f32x4 s0[NB][2];
@@ -721,16 +729,14 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
 
     // Entering tile t (at step 2t): at the start of a group (t % SYNC == 0)
     // tiles t+1 .. t+SYNC must have landed (the earlier ones were waited for
-    // at the previous group); tiles up to t+STAGES-SYNC-1 may still be in
-    // flight.  Once every wave passed the barrier the stages of the previous
-    // group are free for tiles up to t+STAGES-1.
+    // at the previous group); the later issued ones may still be in flight.
+    // Once every wave passed the barrier the stages of the previous group are
+    // free for tiles up to t+STAGES-1.
     auto sync_tile = [&](int t) {
         if (t % SYNC != 0 || t + 1 >= ntot) return;
-        const int last = t == 0 ? STAGES - 1 : t + STAGES - SYNC - 1;  // last tile issued so far
-        wait_tiles<BPW>(max(0, min(last, ntot - 1) - (t + SYNC)));
+        wait_tiles<BPW>(max(0, issued - 1 - (t + SYNC)));
         __builtin_amdgcn_s_barrier();
-        if (t > 0)
-            for (int u = max(t + STAGES - SYNC, t + 1); u < t + STAGES && u < ntot; ++u) copy_tile(u, tile_stage(u));
+        for (; issued < min(t + STAGES, ntot); ++issued) copy_tile(issued, tile_stage(issued));
     };
     // steady state: steps whose successor is neither the last nor masked
     int g = 0;
@@ -763,7 +769,6 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     // the round's tiles of the segments holding its rows, side by side.  The
     // root loop (or the prologue) already issued the first tiles.
     {
-        int issued = min((ntiles > 0 ? (ntiles - 1) / SYNC * SYNC : 0) + STAGES, ntot);
         for (int r0 = ntiles; r0 < ntot; r0 += STAGES) {
             const int r1 = min(r0 + STAGES, ntot);
             __builtin_amdgcn_s_barrier();  // every wave is done with the tiles before r0

@@ -1,6 +1,6 @@
 """Decode-step benchmark of the Qwen3-4B-shaped workload with cached tree-attention plans.
 
-    python -m tree_attention.benchmark_decode [--steps 16] [--layers 36] [--method cube]
+    python -m tree_attention.benchmark_decode [--steps 16] [--layers 36] [--method cube] [--prefill tree]
 
 Counterpart of the reference's scripts/benchmark_decode_plan.py (a cached
 prompt plan whose tails grow by one token per step, :21-64) and
@@ -15,8 +15,14 @@ scripts/benchmark_qwen.py (the model around it), on one MI355X:
   steps of ``CachedPrefixDecoder`` (the prompt is planned once; each step only
   sets the tails' lengths).
 
-It runs the steps twice on two decoders fed the same tokens: with the fused
-per-layer decode glue (RoPE, the pool scatters and the Q layout in one launch,
+Prefill is timed both ways: one full forward per request (the reference
+adapter, qwen.py:34-51) and shared-prefix prefill (every tree node once over
+its ancestors' cache); it reports both times and, against an fp32 forward of
+the same weights (one full prompt per request), the error of each prefill's
+last-token logits, so the two bf16 prefills are compared with the truth rather
+than with each other.  It then runs the steps twice on two decoders
+(prefilled by ``--prefill``) fed the same tokens: with the fused per-layer
+decode glue (RoPE, the pool scatters and the Q layout in one launch,
 ``kernels.decode_append``) and with the eager ops of the reference adapter.
 Per step it reports the wall time (device synchronised on both sides) and the
 per-layer attention time (HIP events around each ``attention_matrix`` call),
@@ -56,18 +62,39 @@ def main(argv=None):
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--method", default="cube")
     ap.add_argument("--warmup", type=int, default=2, help="decode steps run before the timed ones")
+    ap.add_argument("--prefill", default="tree", choices=["tree", "request"], help="prefill of the decoders")
     args = ap.parse_args(argv)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     model = _model(args.layers, dev)
     sequences = shapes.qwen3_4b_workload()
     budget = args.steps + args.warmup
-    t0 = time.perf_counter()
+    prefill_s, prefill_logits = {}, {}
+    for mode in ("request", "tree"):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        probe = integration.CachedPrefixDecoder(model, sequences, budget, args.method, CostModel.mi355x(),
+                                                prefill=mode)
+        torch.cuda.synchronize()
+        prefill_s[mode] = time.perf_counter() - t0
+        prefill_logits[mode] = probe.logits.float()
+        del probe
+    prefill_diff = (prefill_logits["tree"] - prefill_logits["request"]).abs().max().item()
+    with torch.inference_mode():
+        ref_model = _model(args.layers, dev)
+        ref_model.float()
+        truth = torch.stack([ref_model(torch.tensor([s], device=dev), use_cache=False, logits_to_keep=1).logits[0, -1]
+                             for s in sequences])
+        del ref_model
+        torch.cuda.empty_cache()
+    vs_fp32 = {m: {"max_abs": round((l - truth).abs().max().item(), 4),
+                   "rel_l2": round(((l - truth).norm() / truth.norm()).item(), 5),
+                   "argmax_agree": round((l.argmax(-1) == truth.argmax(-1)).float().mean().item(), 4)}
+               for m, l in prefill_logits.items()}
     decoders = {name: integration.CachedPrefixDecoder(model, sequences, budget, args.method, CostModel.mi355x(),
-                                                      fused_glue=fused)
+                                                      fused_glue=fused, prefill=args.prefill)
                 for name, fused in (("fused", True), ("eager", False))}
     torch.cuda.synchronize()
-    prefill_s = time.perf_counter() - t0
 
     original = integration.attention_matrix
     attn_events = []
@@ -107,14 +134,18 @@ def main(argv=None):
         "benchmark": "qwen3_4b_shaped_decode",
         "config": {"layers": args.layers, "requests": len(sequences), "prompt_tree_tokens": decoders["fused"].prefix_size,
                    "method": args.method, "cost_model": "mi355x", "steps": args.steps, "warmup": args.warmup,
-                   "dtype": "bf16", "weights": "random-init"},
+                   "dtype": "bf16", "weights": "random-init", "prefill": args.prefill,
+                   "prompt_tokens": sum(map(len, sequences))},
         "step_ms": {n: round(statistics.median(v), 3) for n, v in step_ms.items()},
         "attention_us_per_layer": {n: round(statistics.median(v), 2) for n, v in attn_us.items()},
         "glue_saving_us_per_layer": round((statistics.median(step_ms["eager"]) - statistics.median(step_ms["fused"]))
                                           * 1e3 / args.layers, 2),
         "fused_equals_eager": identical,
         "plan": {"jobs": len(cached.jobs), "items": list(cached.abi.n_items), "attached": len(cached.attached)},
-        "prefill_s": round(prefill_s, 2),
+        "prefill_s": {m: round(t, 3) for m, t in prefill_s.items()},
+        "prefill_speedup": round(prefill_s["request"] / prefill_s["tree"], 2),
+        "prefill_logits_max_abs_diff": round(prefill_diff, 4),
+        "prefill_logits_vs_fp32": vs_fp32,
     }
     print(json.dumps(line), flush=True)
 

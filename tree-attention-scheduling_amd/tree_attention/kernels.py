@@ -124,7 +124,8 @@ def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256, tails=frozense
 
     Small jobs (<= 16 query rows) get one item per KV head, of kind TA_TAIL for
     the jobs in ``tails`` and TA_SMALL otherwise; larger jobs one per (row
-    tile, KV head), the tile size chosen by ``_large_kind``.
+    tile, KV head), the tile size chosen by ``_large_kind``; TA_LARGE256 items
+    are ordered by KV head, then job, then first row.
     """
     triples = {k: [] for k in (_native.TA_SMALL, *_native.KIND_ROWS, _native.TA_TAIL)}
     for j in range(len(jobs)):
@@ -138,6 +139,10 @@ def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256, tails=frozense
         for h in range(kvheads):
             for row0 in range(0, rows, tile):
                 triples[kind].append((j, row0, h))
+    # The 256-row kernel gives each XCD a contiguous range of items: in head-major
+    # order an XCD works on one KV head, so its L2 holds that head's Q rows and K/V.
+    big = triples[_native.TA_LARGE256]
+    big.sort(key=lambda t: (t[2], t[0], t[1]))
     return {k: np.asarray(v, dtype=np.int32).reshape(-1) for k, v in triples.items()}
 
 

@@ -53,10 +53,15 @@ class SharedKVDecoder:
     ``sequences`` are token-id lists (one per request).  The prompt of every
     request is prefilled with the model's own attention; afterwards every
     ``step`` appends one token per request and re-plans the whole tree
-    (reference qwen.py:58-61,74-103).
+    (reference qwen.py:58-61,74-103).  ``prefill="request"`` runs one full
+    forward per request, as the reference does; ``prefill="tree"`` runs every
+    tree node once over its ancestors' cache (``_prefill_tree``).
     """
 
-    def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None, fused_glue=None):
+    def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None, fused_glue=None,
+                 prefill="request"):
+        if prefill not in ("request", "tree"):
+            raise ValueError("prefill must be 'request' or 'tree'")
         self.model = model
         self.sequences = [list(s) for s in sequences]
         self.tree = KVTree.from_sequences(self.sequences)
@@ -84,7 +89,7 @@ class SharedKVDecoder:
                        torch.empty((self.hk, alloc, self.dim), device=self.device, dtype=dtype))
                       for _ in model.model.layers]
         self.leaves = [_find_leaf(self.tree, r) for r in range(len(self.sequences))]
-        self._prefill()
+        self._prefill_tree() if prefill == "tree" else self._prefill()
 
     # -------------------------------------------------------------- prefill
     @torch.inference_mode()
@@ -106,6 +111,90 @@ class SharedKVDecoder:
                     vp.index_copy_(1, dst, layer.values[0].index_select(1, src))
             written.update(path)
         self.logits = torch.stack(last)
+
+    @torch.inference_mode()
+    def _prefill_tree(self, leaf_batch=16):
+        """Prefill every tree node once, in depth-first order, over its ancestors' cached K/V.
+
+        The reference prefills each request's whole prompt and keeps the first
+        copy of every shared position (qwen.py:34-51): work grows with the sum
+        of the prompt lengths.  Here a node's tokens run through the model once,
+        attending to the cache of the chain above it, so work grows with the
+        stored tokens.  Childless siblings run together, up to ``leaf_batch``
+        per forward, right-padded to the longest over the parent's cache
+        repeated per row (causal attention keeps every real token from the pads
+        after it).  After a node's subtree the cache is cut back to the node's
+        start.  A request's logits are those of the last token of its terminal
+        node.  Positions, causal masking and RoPE are those of the full prompt;
+        only the floating-point order of the reductions differs from one full
+        forward per request.
+        """
+        from transformers import DynamicCache
+
+        nodes = self.tree.nodes
+        last = [None] * len(self.sequences)
+        cache = DynamicCache()
+
+        def cut(cache, base):
+            held = cache.get_seq_length()
+            if base == 0:
+                return DynamicCache()
+            if held > base:
+                cache.crop(base - held)  # drop the tokens after base
+            return cache
+
+        stack = [(0, False, 0)]  # (node, subtree done, cache length before the node)
+        while stack:
+            v, done, base = stack.pop()
+            node = nodes[v]
+            if done:
+                cache = cut(cache, base)
+                continue
+            if node.tokens:
+                cache = self._prefill_nodes([v], base, cache, last)
+            stack.append((v, True, base))
+            held = base + len(node.tokens)
+            leaves = [c for c in node.children if not nodes[c].children]
+            for i in range(0, len(leaves), leaf_batch):
+                cache = self._prefill_nodes(leaves[i:i + leaf_batch], held, cache, last)
+                cache = cut(cache, held)
+            for c in reversed(node.children):
+                if nodes[c].children:
+                    stack.append((c, False, held))
+        self.logits = torch.stack(last)
+
+    def _prefill_nodes(self, group, base, cache, last):
+        """One forward of sibling nodes ``group`` over a batch-1 cache of ``base`` tokens.
+
+        Writes the nodes' K/V into the pools and their terminal requests' logits
+        into ``last``; returns the cache, extended by the group's tokens (batch
+        rows = group members; a one-node group leaves it ready for the node's
+        children).
+        """
+        nodes, ids, dev = self.tree.nodes, self.tree.token_ids, self.device
+        lens = [len(nodes[c].tokens) for c in group]
+        width = max(lens)
+        batch = torch.zeros((len(group), width), dtype=torch.long)
+        for i, c in enumerate(group):
+            batch[i, :lens[i]] = torch.tensor([ids[p] for p in nodes[c].tokens])
+        if len(group) > 1:
+            cache.batch_repeat_interleave(len(group))
+        ends = sorted({n - 1 for n in lens})
+        keep = torch.tensor(ends, device=dev)
+        out = self.model(input_ids=batch.to(dev), past_key_values=cache, use_cache=True, logits_to_keep=keep)
+        cache = out.past_key_values
+        for i, c in enumerate(group):
+            n = lens[i]
+            dst = torch.tensor(nodes[c].tokens, device=dev)
+            for (kp, vp), layer in zip(self.pools, cache.layers):
+                # cache tensors are [batch, HK, positions, D]; this node's are [base, base + n)
+                kp.index_copy_(2, dst, layer.keys[i, :, base:base + n].transpose(1, 2))
+                vp.index_copy_(1, dst, layer.values[i, :, base:base + n])
+            for r in nodes[c].terminal:
+                last[r] = out.logits[i, ends.index(n - 1)].clone()
+        if len(group) > 1:
+            cache.batch_select_indices(torch.tensor([0], device=dev))
+        return cache
 
     # ------------------------------------------------------------ decoding
     def _next_positions(self, count):
@@ -178,8 +267,9 @@ class SharedKVDecoder:
 class CachedPrefixDecoder(SharedKVDecoder):
     """Plans the prompt tree once; each step only sets the decode-tail lengths (qwen.py:106-124)."""
 
-    def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None, fused_glue=None):
-        super().__init__(model, sequences, max_new_tokens, method, cost_model, fused_glue)
+    def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None, fused_glue=None,
+                 prefill="request"):
+        super().__init__(model, sequences, max_new_tokens, method, cost_model, fused_glue, prefill)
         prompt_plan = schedule(self.tree, self.hq, self.hk, self.dim, self.method, self.cost_model)
         shape_of_q = torch.empty((len(self.sequences), self.hq, self.dim), device=self.device,
                                  dtype=model.dtype)
