@@ -76,7 +76,7 @@ def main():
         sys.exit(2)
     import torch
     from tree_attention import CostModel, schedule, shapes
-    from tree_attention import _native
+    from tree_attention import _native, _planner
     from tree_attention.kernels import (attention_matrix, launch_durations_us, merge, pack_kv, prepare, segment,
                                         tail_merge)
 
@@ -94,14 +94,18 @@ def main():
     kp0, vp0 = pack_kv(k.to(dev), v.to(dev))
     pools = [(kp0, vp0)] + [(kp0.clone(), vp0.clone()) for _ in range(POOLS - 1)]
 
-    t0 = time.perf_counter()
-    plan = schedule(tree, HQ, HK, D, args.method, model)
-    plan_us = (time.perf_counter() - t0) * 1e6
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    prepared = prepare(plan, qd)
-    torch.cuda.synchronize()
-    metadata_us = (time.perf_counter() - t0) * 1e6
+    # host planning: the first call (library load, id tuples) and the median of warm calls
+    plan_times, meta_times = [], []
+    for _ in range(6):
+        t0 = time.perf_counter()
+        plan = schedule(tree, HQ, HK, D, args.method, model)
+        plan_times.append((time.perf_counter() - t0) * 1e6)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        prepared = prepare(plan, qd)
+        torch.cuda.synchronize()
+        meta_times.append((time.perf_counter() - t0) * 1e6)
+    plan_us, metadata_us = statistics.median(plan_times[1:]), statistics.median(meta_times[1:])
 
     stream = torch.cuda.current_stream(dev)
 
@@ -260,6 +264,8 @@ def main():
         "kernel_us": {n: round(t, 3) for n, t in kernel_us.items()},
         "kernel_graph_slot_us": {n: round(t, 3) for n, t in kernel_slot_us.items()},
         "plan": {"jobs": len(jobs), "small_jobs": prepared.small_jobs, "plan_us": round(plan_us, 1),
+                 "plan_first_call_us": round(plan_times[0], 1), "metadata_first_call_us": round(meta_times[0], 1),
+                 "planner": "cpp" if _planner.available() else "python",
                  "metadata_us": round(metadata_us, 1), "estimated_us": plan.estimated_us,
                  "small_tokens": small_tokens, "large_flops": large_flops},
         "rel_l2_vs_fp32": rel,
