@@ -132,3 +132,34 @@ def test_uncovered_cases_fall_back_or_raise():
     with pytest.raises(ValueError):
         schedule(tree, method="cube", model=Scaled(), native=True)
     assert schedule(tree, method="cube", model=Scaled()).estimated_us == 2.0 * schedule(tree).estimated_us
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_native_tail_attachment_equals_python(seed):
+    """tp_attach_tails against kernels._attach_tails_py on random job sets: same attachments, same order."""
+    from tree_attention import kernels
+    from tree_attention.schedule import Job
+    rng = random.Random(seed)
+    nreq = rng.randint(4, 300)
+    large, base = [], 0
+    for _ in range(rng.randint(1, 12)):
+        reqs = tuple(sorted(rng.sample(range(nreq), rng.randint(1, nreq))))
+        n = rng.randint(8, 900)
+        large.append(Job(reqs, tuple(range(base, base + n))))
+        base += n
+    small = []
+    for _ in range(rng.randint(0, 200)):
+        reqs = (rng.randrange(nreq),) if rng.random() < 0.85 else tuple(sorted(rng.sample(range(nreq), 2)))
+        n = rng.randint(1, 300)
+        small.append(Job(reqs, tuple(range(base, base + n))))
+        base += n
+    fixed = {id(j) for j in small if rng.random() < 0.1}
+    for group in (1, 4, 8, 16):
+        for tile_rows in (128, 256):
+            args = (small, large, group, tile_rows, lambda j: id(j) in fixed)
+            left, attached = kernels._attach_tails(*args)
+            left_py, attached_py = kernels._attach_tails_py(*args)
+            assert [id(j) for j in left] == [id(j) for j in left_py]
+            assert list(attached) == list(attached_py)
+            for key in attached:
+                assert [(id(j), r) for j, r in attached[key]] == [(id(j), r) for j, r in attached_py[key]]

@@ -368,3 +368,80 @@ extern "C" int tp_grouped_plan(int32_t method, int32_t n, const int32_t *parent,
     total[0] = p.memo[p.key(0, -1)].total;
     return 0;
 }
+
+// Attachment of private tails to 256-row work items (tree_attention/kernels.py
+// _attach_tails): small jobs of one request go, in order, to the candidate
+// item (a 256-row item of a large job whose rows include the request's, all
+// in one wave) with the fewest attached tiles, then the fewest on the owning
+// wave, then the lowest large job, within `xtail_max` segments and the item's
+// own tile count.
+//   large jobs J < n_large: is256[J], tiles[J], requests req[req_off[J] .. req_off[J+1])
+//   small jobs s < n_small: nreq_s[s], first request req0[s], tiles_s[s], fixed[s]
+// Writes item[s] (index into the item list, -1: not attached) and lrow[s]
+// (first job row of the request), the item list (item_job, item_row0) and
+// n_items[0].  Returns 0, or 1 for invalid arguments.
+extern "C" int tp_attach_tails(int32_t n_large, const int32_t *is256, const int32_t *tiles, const int32_t *req_off,
+                               const int32_t *req, int32_t group, int32_t n_small, const int32_t *nreq_s,
+                               const int32_t *req0, const int32_t *tiles_s, const int8_t *fixed, int32_t nreq,
+                               int32_t xtail_max, int32_t wave_rows, int32_t item_rows, int32_t *item,
+                               int32_t *lrow, int32_t *item_job, int32_t *item_row0, int32_t *n_items) {
+    if (n_large < 0 || n_small < 0 || nreq <= 0 || group <= 0 || xtail_max < 0 || wave_rows <= 0 ||
+        item_rows <= 0 || item_rows % wave_rows || (n_large && (!is256 || !tiles || !req_off || !req)) ||
+        (n_small && (!nreq_s || !req0 || !tiles_s || !fixed || !item || !lrow)) || !item_job || !item_row0 ||
+        !n_items)
+        return 1;
+    struct Cand {
+        int32_t job, item, wave, lrow;
+    };
+    std::vector<std::vector<Cand>> holders(nreq);
+    std::vector<int32_t> own;
+    int32_t ni = 0;
+    for (int32_t j = 0; j < n_large; ++j) {
+        if (req_off[j + 1] < req_off[j]) return 1;
+        if (!is256[j]) continue;
+        const int64_t rows = (int64_t)(req_off[j + 1] - req_off[j]) * group;
+        const int32_t first = ni;
+        for (int64_t r0 = 0; r0 < rows; r0 += item_rows) {
+            item_job[ni] = j;
+            item_row0[ni] = (int32_t)r0;
+            own.push_back(tiles[j]);
+            ++ni;
+        }
+        for (int32_t pos = req_off[j]; pos < req_off[j + 1]; ++pos) {
+            const int32_t r = req[pos];
+            if (r < 0 || r >= nreq) return 1;
+            const int32_t lr = (pos - req_off[j]) * group;
+            if (lr % wave_rows + group <= wave_rows)
+                holders[r].push_back({j, first + lr / item_rows, lr % item_rows / wave_rows, lr});
+        }
+    }
+    n_items[0] = ni;
+    const int waves = item_rows / wave_rows;
+    std::vector<int32_t> item_tiles(ni, 0), item_segs(ni, 0), wave_tiles((size_t)ni * waves, 0);
+    for (int32_t s = 0; s < n_small; ++s) {
+        item[s] = -1;
+        lrow[s] = 0;
+        const int32_t r = req0[s];
+        if (nreq_s[s] != 1 || fixed[s] || r < 0 || r >= nreq) continue;
+        const int32_t n = tiles_s[s];
+        const Cand *best = nullptr;
+        int32_t bt = 0, bw = 0;
+        for (const Cand &c : holders[r]) {
+            const int32_t t = item_tiles[c.item];
+            if (item_segs[c.item] >= xtail_max || t + n > own[c.item]) continue;
+            const int32_t w = wave_tiles[(size_t)c.item * waves + c.wave];
+            if (!best || t < bt || (t == bt && (w < bw || (w == bw && c.job < best->job)))) {
+                best = &c;
+                bt = t;
+                bw = w;
+            }
+        }
+        if (!best) continue;
+        item[s] = best->item;
+        lrow[s] = best->lrow;
+        item_tiles[best->item] += n;
+        item_segs[best->item] += 1;
+        wave_tiles[(size_t)best->item * waves + best->wave] += n;
+    }
+    return 0;
+}

@@ -1,21 +1,24 @@
-"""ctypes binding of ``libtree_plan.so``, the host grouped planner (include/tree_plan.h).
+"""ctypes binding of ``libtree_plan.so``, the host planner library (include/tree_plan.h).
 
 ``grouped_decisions`` hands the tree to ``tp_grouped_plan`` in CSR form and
 returns, per node, whether its parent pushes it (the subset-DP / greedy
-decision of the reference's schedule.py:94-131).  The library is a plain host
-library (g++), loaded on first use; ``TREE_PLAN_LIB`` selects another build.
+decision of the reference's schedule.py:94-131).  ``attach_tails`` runs the
+tail-attachment step of ``kernels.prepare`` (``tp_attach_tails``).  The
+library is a plain host library (g++), loaded on first use; ``TREE_PLAN_LIB``
+selects another build.
 """
 from __future__ import annotations
 
 import ctypes
 import os
 import threading
+from itertools import chain
 from pathlib import Path
 
 import numpy as np
 
 LIB_PATH = Path(__file__).with_name("libtree_plan.so")
-EXPORTS = ("tp_grouped_plan",)
+EXPORTS = ("tp_grouped_plan", "tp_attach_tails")
 METHODS = {"greedy": 0, "cube": 1}
 
 _lib = None
@@ -41,6 +44,10 @@ def load(required: bool = True):
             lib = ctypes.CDLL(str(target))
             lib.tp_grouped_plan.restype = ctypes.c_int
             lib.tp_grouped_plan.argtypes = [ctypes.c_int32, ctypes.c_int32] + [_p] * 11
+            i32 = ctypes.c_int32
+            lib.tp_attach_tails.restype = ctypes.c_int
+            lib.tp_attach_tails.argtypes = ([i32, _p, _p, _p, _p, i32, i32, _p, _p, _p, _p, i32, i32, i32, i32]
+                                            + [_p] * 5)
             _lib = lib
     return _lib
 
@@ -84,3 +91,35 @@ def grouped_decisions(tree, method: str, model, qheads: int, kvheads: int, dim: 
     if rc != 0:
         raise ValueError(f"tp_grouped_plan rejected its arguments (code {rc})")
     return pushed, float(total[0])
+
+
+def attach_tails(large, small, group, is256, large_tiles, small_tiles, fixed, nreq, xtail_max, wave_rows,
+                 item_rows):
+    """``tp_attach_tails`` over job lists; returns (item per small job or -1, lrow per small job, item keys)."""
+    lib = load()
+    nl, ns = len(large), len(small)
+    req_off = np.zeros(nl + 1, dtype=np.int32)
+    np.cumsum([len(j.requests) for j in large], out=req_off[1:])
+    req = np.fromiter(chain.from_iterable(j.requests for j in large), dtype=np.int32, count=int(req_off[-1]))
+    is256 = np.asarray(is256, dtype=np.int32)
+    tiles = np.asarray(large_tiles, dtype=np.int32)
+    nreq_s = np.fromiter((len(j.requests) for j in small), dtype=np.int32, count=ns)
+    req0 = np.fromiter((j.requests[0] for j in small), dtype=np.int32, count=ns)
+    tiles_s = np.asarray(small_tiles, dtype=np.int32)
+    fixed = np.asarray(fixed, dtype=np.int8)
+    cap = int(sum(-(-len(j.requests) * group // item_rows) for j, b in zip(large, is256) if b))
+    item = np.zeros(max(ns, 1), dtype=np.int32)
+    lrow = np.zeros(max(ns, 1), dtype=np.int32)
+    item_job = np.zeros(max(cap, 1), dtype=np.int32)
+    item_row0 = np.zeros(max(cap, 1), dtype=np.int32)
+    n_items = np.zeros(1, dtype=np.int32)
+    one = np.zeros(1, dtype=np.int32)
+    ptr = lambda a: _ptr(a if a.size else one)  # noqa: E731
+    rc = lib.tp_attach_tails(nl, ptr(is256), ptr(tiles), _ptr(req_off), ptr(req), group, ns, ptr(nreq_s), ptr(req0),
+                             ptr(tiles_s), _ptr(fixed if fixed.size else np.zeros(1, np.int8)), nreq, xtail_max,
+                             wave_rows, item_rows, _ptr(item), _ptr(lrow), _ptr(item_job), _ptr(item_row0),
+                             _ptr(n_items))
+    if rc != 0:
+        raise ValueError(f"tp_attach_tails rejected its arguments (code {rc})")
+    keys = list(zip(item_job[:n_items[0]].tolist(), item_row0[:n_items[0]].tolist()))
+    return item[:ns].tolist(), lrow[:ns].tolist(), keys

@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass, field
+from itertools import chain
 
 import numpy as np
 import torch
@@ -127,23 +128,42 @@ def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256, tails=frozense
     tile, KV head), the tile size chosen by ``_large_kind``; TA_LARGE256 items
     are ordered by KV head, then job, then first row.
     """
-    triples = {k: [] for k in (_native.TA_SMALL, *_native.KIND_ROWS, _native.TA_TAIL)}
-    for j in range(len(jobs)):
-        rows = len(jobs[j].requests) * group
-        if j < small_jobs:
-            kind = _native.TA_TAIL if j in tails else _native.TA_SMALL
-            triples[kind].extend((j, 0, h) for h in range(kvheads))
-            continue
-        kind = _large_kind(rows, tile_rows)
-        tile = _native.KIND_ROWS[kind]
-        for h in range(kvheads):
-            for row0 in range(0, rows, tile):
-                triples[kind].append((j, row0, h))
-    # The 256-row kernel gives each XCD a contiguous range of items: in head-major
-    # order an XCD works on one KV head, so its L2 holds that head's Q rows and K/V.
-    big = triples[_native.TA_LARGE256]
-    big.sort(key=lambda t: (t[2], t[0], t[1]))
-    return {k: np.asarray(v, dtype=np.int32).reshape(-1) for k, v in triples.items()}
+    def triples(job, row0, head):
+        return np.stack([job, row0, head], axis=1).astype(np.int32).reshape(-1)
+
+    heads = np.arange(kvheads)
+    out = {}
+    small = np.arange(small_jobs)
+    is_tail = np.isin(small, np.fromiter(tails, dtype=np.int64, count=len(tails)))
+    for kind, sel in ((_native.TA_SMALL, ~is_tail), (_native.TA_TAIL, is_tail)):
+        js = small[sel]  # one item per (job, KV head), job-major
+        out[kind] = triples(np.repeat(js, kvheads), np.zeros(js.size * kvheads, dtype=np.int64),
+                            np.tile(heads, js.size))
+    big = np.arange(small_jobs, len(jobs))
+    rows = np.fromiter((len(jobs[j].requests) * group for j in big), dtype=np.int64, count=big.size)
+    kinds = np.where((rows <= 64) | (tile_rows <= 64), _native.TA_LARGE64,
+                     np.where((rows <= 128) | (tile_rows <= 128), _native.TA_LARGE128, _native.TA_LARGE256))
+    for kind, tile in _native.KIND_ROWS.items():
+        js = big[kinds == kind]
+        ntile = -(-rows[kinds == kind] // tile)
+        if kind == _native.TA_LARGE256:
+            # The 256-row kernel gives each XCD a contiguous range of items: in
+            # head-major order an XCD works on one KV head, so its L2 holds that
+            # head's Q rows and K/V.  Order: head, job, first row.
+            n = int(ntile.sum())
+            within = np.arange(n) - np.repeat(np.cumsum(ntile) - ntile, ntile)
+            job = np.tile(np.repeat(js, ntile), kvheads)
+            first = np.tile(within * tile, kvheads)
+            head = np.repeat(heads, n)
+        else:  # job, head, first row
+            per_job = ntile * kvheads
+            within = np.arange(int(per_job.sum())) - np.repeat(np.cumsum(per_job) - per_job, per_job)
+            nt = np.repeat(ntile, per_job)
+            job = np.repeat(js, per_job)
+            head = within // np.maximum(nt, 1)
+            first = within % np.maximum(nt, 1) * tile
+        out[kind] = triples(job, first, head)
+    return out
 
 
 TOKEN_QUANTUM = 64  # tokens per LDS tile of the segment kernels
@@ -158,6 +178,30 @@ def _tiles(job) -> int:
 
 
 def _attach_tails(small, large, group, tile_rows, is_fixed):
+    """``_attach_tails_py`` through the host library (``tp_attach_tails``) when it is built.
+
+    Both give the same attachments in the same order.
+    """
+    from . import _planner
+    if not small or not large or not _planner.available():
+        return _attach_tails_py(small, large, group, tile_rows, is_fixed)
+    is256 = [_large_kind(len(j.requests) * group, tile_rows) == _native.TA_LARGE256 for j in large]
+    if not any(is256):
+        return small, {}
+    nreq = 1 + max(max(j.requests) for j in (*large, *small))
+    item, lrow, keys = _planner.attach_tails(
+        large, small, group, is256, [_tiles(j) for j in large], [_tiles(j) for j in small],
+        [bool(is_fixed(j)) for j in small], nreq, XTAIL_MAX, WAVE_ROWS, 256)
+    attached, left = {}, []
+    for job, it, lr in zip(small, item, lrow):
+        if it < 0:
+            left.append(job)
+        else:
+            attached.setdefault(keys[it], []).append((job, lr))
+    return left, attached
+
+
+def _attach_tails_py(small, large, group, tile_rows, is_fixed):
     """Fold single-request small jobs into TA_LARGE256 work items of large jobs.
 
     A small job of one request ``r`` (a private tail) can be attended by any
@@ -241,15 +285,29 @@ def _recut(jobs, items_per_chunk, target_items, is_fixed):
         else:
             runs.append([job.requests, t0, n, fixed])
 
-    def count(limit):
-        return sum(items_per_chunk(r) * (1 if f else -(-n // limit)) for r, _, n, f in runs)
+    weights = [(items_per_chunk(r), n, f) for r, _, n, f in runs]
+    fixed_items = sum(w for w, _, f in weights if f)
+    cut = [(w, n) for w, n, f in weights if not f]
 
-    longest = max((n for _, _, n, f in runs if not f), default=0)
+    def count(limit):  # work items at a chunk limit; non-increasing in limit
+        return fixed_items + sum(w * -(-n // limit) for w, n in cut)
+
+    longest = max((n for _, n in cut), default=0)
     if longest == 0:
         return jobs
-    limit = -(-longest // TOKEN_QUANTUM) * TOKEN_QUANTUM
-    while limit > TOKEN_QUANTUM and count(limit) < target_items:
-        limit -= TOKEN_QUANTUM
+    # the longest limit (a multiple of TOKEN_QUANTUM, at most the longest run)
+    # that still gives target_items, else TOKEN_QUANTUM: binary search over the
+    # multiples, count being monotone
+    lo, hi = 1, -(-longest // TOKEN_QUANTUM)
+    if count(hi * TOKEN_QUANTUM) >= target_items:
+        lo = hi
+    while hi - lo > 1:  # count(lo) >= target_items or lo == 1; count(hi) < target_items
+        mid = (lo + hi) // 2
+        if count(mid * TOKEN_QUANTUM) >= target_items:
+            lo = mid
+        else:
+            hi = mid
+    limit = lo * TOKEN_QUANTUM
     out = []
     for reqs, t0, n, fixed in runs:
         if fixed:
@@ -325,54 +383,67 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     jobs = small + large
     small_jobs = len(small)
     njobs = len(jobs)
-    maxr = max(len(j.requests) for j in jobs)
+    qlen = np.fromiter((len(j.requests) for j in jobs), dtype=np.int32, count=njobs)
+    klen = np.fromiter((len(j.tokens) for j in jobs), dtype=np.int32, count=njobs)
+    kids = np.fromiter((j.tokens[0] for j in jobs), dtype=np.int32, count=njobs).reshape(njobs, 1)
+    ends = np.cumsum(qlen)
+    rowbase = (ends - qlen).astype(np.int32)  # partial slot of each job's first request
+    nslot = int(ends[-1])
+    flat = np.fromiter(chain.from_iterable(j.requests for j in jobs), dtype=np.int64, count=nslot)
+    bad = np.flatnonzero((flat < 0) | (flat >= nreq))
+    if bad.size:
+        i = int(np.searchsorted(ends, bad[0], side="right"))
+        raise ValueError(f"Job {i} names request {int(flat[bad[0]])} outside q's {nreq} requests")
+    maxr = int(qlen.max())
+    local = np.arange(nslot) - np.repeat(rowbase, qlen)  # request's row within its job
     qids = np.zeros((njobs, maxr), dtype=np.int32)
-    kids = np.zeros((njobs, 1), dtype=np.int32)
-    qlen = np.zeros(njobs, dtype=np.int32)
-    klen = np.zeros(njobs, dtype=np.int32)
-    rowbase = np.zeros(njobs, dtype=np.int32)
-    slots = [[] for _ in range(nreq)]
-    nslot = 0
-    for i, job in enumerate(jobs):
-        reqs, toks = job.requests, job.tokens
-        qids[i, :len(reqs)] = reqs
-        kids[i, 0] = toks[0]
-        qlen[i] = len(reqs)
-        klen[i] = len(toks)
-        rowbase[i] = nslot
-        for local, r in enumerate(reqs):
-            if not 0 <= r < nreq:
-                raise ValueError(f"Job {i} names request {r} outside q's {nreq} requests")
-            slots[r].append(nslot + local)
-        nslot += len(reqs)
-    tails = _tail_jobs(jobs, small_jobs)
-    for j in tails:  # a tail job's slot goes last: its work item merges the others first
-        r, own = jobs[j].requests[0], int(rowbase[j])
-        slots[r].remove(own)
-        slots[r].append(own)
-    maxs = max(1, max(map(len, slots)))
+    qids[np.repeat(np.arange(njobs), qlen), local] = flat
+    # each request's slots in job order: slot s holds request flat[s]
+    counts = np.bincount(flat, minlength=nreq).astype(np.int32)
+    maxs = max(1, int(counts.max()))
+    order = np.argsort(flat, kind="stable")
+    rank = np.arange(nslot) - np.repeat(np.cumsum(counts) - counts, counts)
     slot_array = np.zeros((nreq, maxs), dtype=np.int32)
-    for r, values in enumerate(slots):
-        slot_array[r, :len(values)] = values
-    counts = np.array([len(s) for s in slots], dtype=np.int32)
+    slot_array[flat[order], rank] = order
+    tails = _tail_jobs(jobs, small_jobs)
+    tail_list = sorted(tails)
+    tail_req = np.array([jobs[j].requests[0] for j in tail_list], dtype=np.int64)
+    if tail_req.size:
+        # A tail job's slot goes last: its work item merges the request's other
+        # slots first.  Small jobs come first, so it is the request's first slot.
+        rows = slot_array[tail_req]
+        assert (rows[:, 0] == rowbase[tail_list]).all()
+        c = counts[tail_req][:, None]
+        k = np.arange(maxs)[None, :]
+        src = np.where(k < c - 1, k + 1, np.where(k == c - 1, 0, k))
+        slot_array[tail_req] = np.take_along_axis(rows, src, 1)
     items = _build_items(jobs, small_jobs, group, kvheads, tile_rows, tails)
-    tail_requests = {jobs[j].requests[0] for j in tails}
-    rest = np.array([r for r in range(nreq) if r not in tail_requests], dtype=np.int32)
+    rest = np.setdiff1d(np.arange(nreq, dtype=np.int32), tail_req.astype(np.int32))
     # attached segments of each TA_LARGE256 item: count, then (first token, tokens, first job row)
+    # (one record per (job, first row), shared by the item of every KV head)
     xstride = 1 + 3 * XTAIL_MAX
-    big = items[_native.TA_LARGE256].reshape(-1, 3)
-    xtail = np.zeros((len(big), xstride), dtype=np.int32)
-    for i, (j, row0, _) in enumerate(big.tolist()):
-        segs = attached.get((j - small_jobs, row0), ())
-        xtail[i, 0] = len(segs)
-        for k, (job, lrow) in enumerate(segs):
-            xtail[i, 1 + 3 * k: 4 + 3 * k] = (job.tokens[0], len(job.tokens), lrow)
-    if not attached:
+    if attached:
+        recs = np.zeros((len(attached), xstride), dtype=np.int32)
+        codes = np.zeros(len(attached), dtype=np.int64)
+        for i, ((j, row0), segs) in enumerate(attached.items()):
+            rec = [len(segs)] + [x for job, lrow in segs for x in (job.tokens[0], len(job.tokens), lrow)]
+            recs[i, :len(rec)] = rec
+            codes[i] = (j + small_jobs) << 32 | row0
+        big = items[_native.TA_LARGE256].reshape(-1, 3).astype(np.int64)
+        item_codes = big[:, 0] << 32 | big[:, 1]
+        order = np.argsort(codes)
+        pos = np.minimum(np.searchsorted(codes[order], item_codes), len(codes) - 1)
+        hit = codes[order][pos] == item_codes
+        xtail = np.zeros((len(big), xstride), dtype=np.int32)
+        xtail[hit] = recs[order[pos[hit]]]
+    else:
         xtail = np.zeros((0, xstride), dtype=np.int32)
 
     # first request of each job over consecutive requests, else -1 (kernels.py:23-26, 138)
-    qbase = np.array([j.requests[0] if j.requests == id_run(j.requests[0], j.requests[0] + len(j.requests))
-                      else -1 for j in jobs], dtype=np.int32)
+    breaks = np.zeros(nslot, dtype=np.int64)
+    breaks[1:] = np.cumsum(np.diff(flat) != 1)  # steps other than +1 up to each slot
+    consecutive = breaks[ends - 1] == breaks[rowbase]
+    qbase = np.where(consecutive, flat[rowbase], -1).astype(np.int32)
 
     arrays = ([qids, kids, qlen, klen, slot_array, counts, rowbase, rest, xtail, qbase]
               + [items[k] for k in sorted(items)])
@@ -384,7 +455,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
         offset += array.size
     qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t, rest_t, xtail_t, qbase_t = views[:10]
     item_views = dict(zip(sorted(items), views[10:]))
-    contiguous_q = all(j.requests[-1] - j.requests[0] + 1 == len(j.requests) for j in jobs)
+    contiguous_q = bool((flat[ends - 1] - flat[rowbase] + 1 == qlen).all())
     # partial rows: fp16 scaled by 2^-e per row; lse holds (log-sum-exp, e) per row
     part = torch.empty((nslot, hq, dim), device=dev, dtype=torch.float16)
     lse = torch.empty((nslot, hq, 2), device=dev, dtype=torch.float32)
