@@ -60,7 +60,7 @@ extern "C" {
 #define TA_XTAIL_STRIDE (1 + 3 * TA_XTAIL_MAX)
 
 #define TA_ERR_ARG 1001      /* null pointer, bad size or unsupported shape */
-#define TA_ERR_ALIGN 1002    /* q / kp / vp / part / out not 16-byte aligned */
+#define TA_ERR_ALIGN 1002    /* q / kp / vp / part / out not 16-byte aligned, lse not 8-byte */
 #define TA_ERR_DTYPE 1003    /* dtype not TA_BF16 / TA_FP16 */
 
 /* Everything one attention_matrix call needs besides q, kp, vp and out.

@@ -431,67 +431,79 @@ __global__ __launch_bounds__(64 * NW) void seg_large_kernel(SegParams p) {
 }
 
 // ------------------------------------------------------------------ merge
-// One workgroup per (request, group of MH query heads); thread (head, d4)
-// owns four head-dim elements of one query head.  The slot list is uniform
-// per workgroup (scalar loads), and each thread reads the log-sum-exp and the
-// 8-byte partial slice (four fp16 values) of MERGE_CHUNK slots at once and
-// merges them online in registers: slots -> (lse, partials) is the only chain
-// of dependent memory round trips; no LDS and no barriers.
+// One workgroup of MERGE_NT threads per (request, group of MH query heads);
+// thread (head, d8) owns eight head-dim elements of one query head.  The slot
+// list is uniform per workgroup (scalar loads), and each thread reads, for
+// MERGE_CHUNK slots at once, the 16-byte partial slice (eight fp16 values) and
+// the 8-byte (log-sum-exp, exponent) pair, then merges them online in
+// registers: slots -> (lse, partials) is the only chain of dependent memory
+// round trips; no LDS and no barriers.
 constexpr int MERGE_CHUNK = 16;
+constexpr int MERGE_NT = 128;
 
 template <int D, bool FP16>
-__global__ __launch_bounds__(NT) void merge_kernel(const u16 *__restrict__ part, const float *__restrict__ lse,
-                                                   const int32_t *__restrict__ slots,
-                                                   const int32_t *__restrict__ counts,
-                                                   const int32_t *__restrict__ reqs, u16 *__restrict__ out,
-                                                   int hq, int maxs) {
-    constexpr int TPH = D / 4;    // threads per head
-    constexpr int MH = NT / TPH;  // heads per workgroup
+__global__ __launch_bounds__(MERGE_NT) void merge_kernel(const u16 *__restrict__ part, const float *__restrict__ lse,
+                                                         const int32_t *__restrict__ slots,
+                                                         const int32_t *__restrict__ counts,
+                                                         const int32_t *__restrict__ reqs, u16 *__restrict__ out,
+                                                         int hq, int maxs) {
+    constexpr int TPH = D / 8;          // threads per head
+    constexpr int MH = MERGE_NT / TPH;  // heads per workgroup
     constexpr float LOG2E = 1.44269504088896341f;
     const int r = reqs ? reqs[blockIdx.x] : blockIdx.x;
     const int tid = threadIdx.x;
-    const int hl = tid / TPH, d4 = tid % TPH;
+    const int hl = tid / TPH, d8 = tid % TPH;
     const int head = blockIdx.y * MH + hl;
     if (head >= hq) return;
     const int cnt = counts[r];
     const int32_t *slr = slots + (size_t)r * maxs;
-    const u16 *src = part + (size_t)head * D + 4 * d4;
+    const u16 *src = part + (size_t)head * D + 8 * d8;
+    const float2 *lse2 = reinterpret_cast<const float2 *>(lse) + head;
     const size_t srow = (size_t)hq * D;
 
     float M = NEG_INF, Z = 0.f;  // running max (log2 units) and weight sum
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
     for (int s0 = 0; s0 < cnt; s0 += MERGE_CHUNK) {
-        float l[MERGE_CHUNK];
-        int e[MERGE_CHUNK];
-        f32x4 v[MERGE_CHUNK];
+        float2 le[MERGE_CHUNK];
+        u32x4 v[MERGE_CHUNK];
 #pragma unroll
         for (int u = 0; u < MERGE_CHUNK; ++u) {
             const int sl = slr[min(s0 + u, cnt - 1)];
-            const size_t prow = (size_t)sl * hq + head;
-            l[u] = s0 + u < cnt ? lse[2 * prow] * LOG2E : NEG_INF;
-            e[u] = (int)lse[2 * prow + 1];
-            v[u] = unpack_f16x4(*(const u32x2 *)(src + sl * srow));
+            le[u] = lse2[(size_t)sl * hq];
+            v[u] = *(const u32x4 *)(src + sl * srow);
         }
+        float l[MERGE_CHUNK];
         float cm = M;
 #pragma unroll
-        for (int u = 0; u < MERGE_CHUNK; ++u) cm = fmaxf(cm, l[u]);
+        for (int u = 0; u < MERGE_CHUNK; ++u) {
+            l[u] = s0 + u < cnt ? le[u].x * LOG2E : NEG_INF;
+            cm = fmaxf(cm, l[u]);
+        }
         if (cm == NEG_INF) continue;  // every slot so far is empty
         if (cm > M) {
             const float alpha = fast_exp2(M - cm);  // 0 while M is -inf
             Z *= alpha;
-            acc *= alpha;
+            lo *= alpha;
+            hi *= alpha;
             M = cm;
         }
 #pragma unroll
         for (int u = 0; u < MERGE_CHUNK; ++u) {
             const float w = fast_exp2(l[u] - M);  // 0 for empty slots
             Z += w;
-            acc += __builtin_amdgcn_ldexpf(w, e[u]) * v[u];
+            const float ws = __builtin_amdgcn_ldexpf(w, (int)le[u].y);
+            lo += ws * unpack_f16x4(u32x2{v[u][0], v[u][1]});
+            hi += ws * unpack_f16x4(u32x2{v[u][2], v[u][3]});
         }
     }
-    if (Z > 0.f) acc *= 1.f / Z;
-    u16 *dst = out + ((size_t)r * hq + head) * D + 4 * d4;
-    *(u32x2 *)dst = u32x2{Ops<FP16>::pack(acc[0], acc[1]), Ops<FP16>::pack(acc[2], acc[3])};
+    if (Z > 0.f) {
+        const float inv = 1.f / Z;
+        lo *= inv;
+        hi *= inv;
+    }
+    u16 *dst = out + ((size_t)r * hq + head) * D + 8 * d8;
+    *(u32x4 *)dst = u32x4{Ops<FP16>::pack(lo[0], lo[1]), Ops<FP16>::pack(lo[2], lo[3]), Ops<FP16>::pack(hi[0], hi[1]),
+                          Ops<FP16>::pack(hi[2], hi[3])};
 }
 
 // ------------------------------------------------------------------ launch
@@ -534,8 +546,8 @@ hipError_t launch_segment(const SegParams &sp, int kind, hipStream_t stream) {
 template <int D, bool FP16>
 hipError_t launch_merge(const void *part, const float *lse, const int32_t *slots, const int32_t *counts,
                         const int32_t *reqs, void *out, int nreq, int hq, int maxs, hipStream_t stream) {
-    constexpr int MH = NT / (D / 4);
-    TA_LAUNCH((merge_kernel<D, FP16>), dim3(nreq, (hq + MH - 1) / MH), dim3(NT), stream,
+    constexpr int MH = MERGE_NT / (D / 8);
+    TA_LAUNCH((merge_kernel<D, FP16>), dim3(nreq, (hq + MH - 1) / MH), dim3(MERGE_NT), stream,
               static_cast<const u16 *>(part), lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs);
     return hipGetLastError();
 }
@@ -568,7 +580,7 @@ const char *ta_error_string(int code) {
     switch (code) {
         case 0: return "success";
         case TA_ERR_ARG: return "tree_attn: invalid argument (null pointer, size or unsupported shape)";
-        case TA_ERR_ALIGN: return "tree_attn: q/kp/vp/part/out must be 16-byte aligned";
+        case TA_ERR_ALIGN: return "tree_attn: q/kp/vp/part/out must be 16-byte aligned, lse 8-byte aligned";
         case TA_ERR_DTYPE: return "tree_attn: dtype must be TA_BF16 or TA_FP16";
         default: return hipGetErrorString((hipError_t)code);
     }
@@ -663,7 +675,7 @@ int ta_merge(const void *part, const float *lse, const int32_t *slots, const int
     if (dtype != TA_BF16 && dtype != TA_FP16) return TA_ERR_DTYPE;
     if (nreq <= 0 || hq <= 0 || maxs <= 0 || (d != 32 && d != 64 && d != 128)) return TA_ERR_ARG;
     if (!part || !lse || !slots || !counts || !out) return TA_ERR_ARG;
-    if (!aligned16(part) || !aligned16(out)) return TA_ERR_ALIGN;
+    if (!aligned16(part) || !aligned16(out) || (reinterpret_cast<uintptr_t>(lse) & 7)) return TA_ERR_ALIGN;
     const hipStream_t st = static_cast<hipStream_t>(stream);
 #define TA_MRG(D, F) launch_merge<D, F>(part, lse, slots, counts, nullptr, out, nreq, hq, maxs, st)
     return (int)TA_DISPATCH(d, dtype == TA_FP16, TA_MRG);
@@ -712,7 +724,7 @@ int ta_attention_matrix(const void *q, const void *kp, const void *vp, int32_t t
         return TA_ERR_ARG;
     if (plan->dtype != TA_BF16 && plan->dtype != TA_FP16) return TA_ERR_DTYPE;
     if (plan->maxs <= 0 || (plan->d != 32 && plan->d != 64 && plan->d != 128)) return TA_ERR_ARG;
-    if (!aligned16(plan->part) || !aligned16(out)) return TA_ERR_ALIGN;
+    if (!aligned16(plan->part) || !aligned16(out) || (reinterpret_cast<uintptr_t>(plan->lse) & 7)) return TA_ERR_ALIGN;
     const hipStream_t st = static_cast<hipStream_t>(stream);
 #define TA_MRG(D, F) \
     launch_merge<D, F>(plan->part, plan->lse, plan->slots, plan->counts, plan->rest, out, plan->n_rest, plan->hq, \
