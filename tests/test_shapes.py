@@ -1,4 +1,6 @@
 """Evaluation and calibration tree shapes (tree_attention.shapes)."""
+import pytest
+
 from tree_attention import shapes
 
 
@@ -69,3 +71,24 @@ def test_grid_comparisons_geometric_mean():
     assert abs(r["geometric_mean_speedup"] - (4 * 9 * 0.5) ** (1 / 3)) < 1e-12
     assert r["median_speedup"] == 4.0 and r["range"] == [0.5, 9.0] and r["faster_shapes"] == 2
     assert c["refresh_us_vs_greedy"]["shapes"] == 3
+
+
+def test_decode_plan_aggregate_matches_reference_schema():
+    """benchmark_decode_plan.aggregate follows scripts/analyze_planning.py:19-39 (decode): per
+    (method, mode), the mean over steps per seed, then median and [min, max] over seeds."""
+    pytest.importorskip("torch")
+    from tree_attention.benchmark_decode_plan import aggregate
+
+    def run(seed, scale):
+        steps = [{"step": i + 1, "planning_us": scale * (i + 1), "kernel_us": 10.0 * scale,
+                  "total_us": scale * (i + 1) + 10.0 * scale} for i in range(4)]
+        return {"method": "cube", "mode": "cached", "seed": seed, "initial_plan_us": 100.0 * scale,
+                "steps": steps, "amortized_us": (100.0 * scale + sum(s["total_us"] for s in steps)) / 4}
+
+    rows = aggregate([run(301, 1.0), run(302, 2.0), run(303, 3.0)])
+    assert len(rows) == 1
+    row = rows[0]
+    assert (row["method"], row["mode"], row["seeds"]) == ("cube", "cached", [301, 302, 303])
+    assert row["planning_us"] == 5.0 and row["planning_us_range"] == [2.5, 7.5]  # mean of 1..4 is 2.5 per unit
+    assert row["kernel_us"] == 20.0 and row["kernel_us_range"] == [10.0, 30.0]
+    assert row["initial_plan_us"] == 200.0 and row["amortized_us_range"][0] == (100.0 + 10.0 + 40.0) / 4
