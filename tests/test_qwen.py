@@ -122,6 +122,21 @@ def test_tree_prefill_matches_request_prefill_cpu():
         integration.SharedKVDecoder(model, SEQUENCES, 2, "cube", prefill="batch")
 
 
+@pytest.mark.parametrize("seqs", [[[1, 2], [3, 4, 5], [6]], [[9]], [[1, 2, 3], [1, 2, 3]],
+                                  [[4, 5], [4, 6, 7], [8, 9], [10]]])
+def test_tree_prefill_edge_trees_cpu(seqs):
+    """Childless nodes batched straight under the root (an empty cache repeated per row), a
+    single one-token prompt and duplicate prompts."""
+    model = tiny_model(torch.float32, "cpu")
+    a = integration.SharedKVDecoder(model, seqs, 2, "cube", prefill="request")
+    b = integration.SharedKVDecoder(model, seqs, 2, "cube", prefill="tree")
+    torch.testing.assert_close(b.logits, full_forward_logits(model, seqs, "cpu"), atol=1e-5, rtol=1e-5)
+    n = a.prefix_size
+    for (ka, va), (kb, vb) in zip(a.pools, b.pools):
+        torch.testing.assert_close(kb[..., :n], ka[..., :n], atol=1e-5, rtol=1e-5)
+        torch.testing.assert_close(vb[:, :n], va[:, :n], atol=1e-5, rtol=1e-5)
+
+
 # four childless siblings of lengths 1-3 under one node, next to inner nodes and a lone leaf
 BRANCHY = [[5, 6, 1], [5, 6, 2, 3], [5, 6, 4, 4, 4], [5, 6, 7], [5, 9, 9], [8], [5, 6, 2, 3]]
 
