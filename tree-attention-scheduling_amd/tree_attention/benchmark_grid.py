@@ -1,12 +1,14 @@
 """Planner comparison over a grid of tree shapes (counterpart of scripts/benchmark_tree_grid.py
 and the comparison block of scripts/analyze_planning.py:60-64).
 
-    python -m tree_attention.benchmark_grid [--grid config|reference] [--iters 10]
+    python -m tree_attention.benchmark_grid [--grid config|reference|nested] [--iters 10]
         [--cost-model mi355x|reference] [--output PATH]
 
 ``--grid config`` (default) is the 81-shape requests x context x shared fraction x
 depth factorial of ``shapes.config_grid``; ``--grid reference`` is the reference's own
-81 trees (``shapes.reference_grid``, scripts/tree_shapes.py:5-19).  Every shape runs
+81 trees (``shapes.reference_grid``, scripts/tree_shapes.py:5-19); ``--grid nested`` is the
+one nested unequal-prefix tree of ``shapes.nested_unequal`` (root 4096 -> 8 x 1024 -> 32 x 256,
+a request ending at an inner node, two duplicate paths).  Every shape runs
 the four planning methods on one MI355X with bf16 Q/K/V ~ N(0, 1) from ``--seed``,
 32 Q / 8 KV heads, d = 128.
 
@@ -106,7 +108,7 @@ def comparisons(rows):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--grid", default="config", choices=["config", "reference"])
+    ap.add_argument("--grid", default="config", choices=["config", "reference", "nested"])
     ap.add_argument("--iters", type=int, default=10)
     ap.add_argument("--seed", type=int, default=201)
     ap.add_argument("--cost-model", default="mi355x", choices=["mi355x", "reference"])
@@ -115,7 +117,10 @@ def main(argv=None):
     args = ap.parse_args(argv)
     dev = torch.device("cuda:0")
     model = CostModel.mi355x() if args.cost_model == "mi355x" else CostModel()
-    grid = list(shapes.config_grid() if args.grid == "config" else shapes.reference_grid())
+    if args.grid == "nested":
+        grid = [({"tree": "nested_unequal"}, shapes.nested_unequal())]
+    else:
+        grid = list(shapes.config_grid() if args.grid == "config" else shapes.reference_grid())
     if args.limit:
         grid = grid[:args.limit]
     # one untimed pass over the first shape: library loads and first calls stay out of the rows
