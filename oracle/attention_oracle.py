@@ -1,9 +1,9 @@
 """CPU oracle for tree-shared decode attention -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this module, and only as the checker (or as the timed
-CPU baseline).  The product path (``tree_attention.kernels``) never calls it and
-fails loudly when the HIP library is missing.
+``bench.py`` may import this module, and only to check results against it (or
+as the timed CPU baseline).  The product path (``tree_attention.kernels``) never
+calls it and fails loudly when the HIP library is missing.
 
 Restates the reference's FP32 oracle ``src/tree_attention/reference.py``:
 
