@@ -98,6 +98,11 @@ typedef struct ta_plan {
      * consecutive (qids[j*maxr + i] == qbase[j] + i), -1 for the others
      * (cf. the reference's contiguous-Q path, kernels.py:23-26, 138). */
     const int32_t *qbase;
+    /* 0, or the stride of an affine slot layout: every merged request r has
+     * maxs partial slots, slot k being r + k * slot_stride (slots[r*maxs + k]
+     * holds the same values).  The merge then computes the slots instead of
+     * loading counts and slot lists. */
+    int32_t slot_stride;
 } ta_plan;
 
 /* Version string of the library build. */
@@ -140,6 +145,11 @@ int ta_attention_matrix(const void *q, const void *kp, const void *vp,
  * (kernels.py:58-83).  Needs tcap % 8 == 0 (TA_ERR_ARG otherwise). */
 int ta_tail_merge(const void *q, const void *kp, const void *vp,
                   int32_t tcap, const ta_plan *plan, void *out, void *stream);
+
+/* The merge of a prepared plan: every request's partial slots into `out`
+ * (kernels.py:166-167), with the plan's affine slot layout (slot_stride) when
+ * it has one -- the merge ta_attention_matrix runs, for all nreq requests. */
+int ta_merge_plan(const ta_plan *plan, void *out, void *stream);
 
 /* One segment launch of a prepared plan: the work items of `kind`, writing
  * partials (TA_TAIL items included), with the plan's attached segments for

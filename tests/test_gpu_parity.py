@@ -278,6 +278,28 @@ def test_large_jobs_over_scattered_requests(device):
     check(out, oracle_fp32(q, k, v, tree), 0.008, 0.03, "scattered")
 
 
+def test_affine_slot_merge_equals_slot_lists(device):
+    """The merge with computed slots (ta_plan.slot_stride) gives the bits of the merge that
+    loads the slot lists, in the layer and through ta_merge_plan / ta_merge."""
+    tree = shapes.tree(shapes.headline())
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 29)
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    prepared = prepare(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), qd)
+    stride = prepared.abi.slot_stride
+    assert stride > 0
+    with_stride = attention_matrix(qd, kp, vp, prepared).clone()
+    merged = merge(prepared).clone()
+    prepared.abi.slot_stride = 0
+    lists = attention_matrix(qd, kp, vp, prepared).clone()
+    merged_lists = merge(prepared).clone()
+    prepared.abi.slot_stride = stride
+    torch.cuda.synchronize()
+    assert torch.equal(with_stride, lists)
+    assert torch.equal(merged, merged_lists) and torch.equal(merged, with_stride)
+    check(with_stride.cpu(), oracle_fp32(q, k, v, tree), 0.008, 0.03, "affine slots")
+
+
 @pytest.mark.parametrize("vscale", [1e5, 1e-5])
 def test_partial_rows_keep_range(vscale, device):
     """Partial rows are fp16 scaled by 2^-e per row: V far outside fp16's range

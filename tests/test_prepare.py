@@ -211,3 +211,22 @@ def test_attachment_limits():
     p = prepare(Plan([root, Job((1,), (300, 301)), Job((2,), (302, 303))], "x", 0.0, settings), q)
     assert [(job.requests, lrow) for segs in p.attached.values() for job, lrow in segs] == [((1,), 12)]
     assert [job.requests for job in p.jobs[:p.small_jobs]] == [(2,)]
+
+
+def test_affine_slot_layout():
+    """The headline plan's slots are affine (request r's slot k is r + k * 128): prepare
+    passes the stride, and the slot lists it still uploads hold exactly those values.
+    Plans with ragged slot lists keep slot_stride 0."""
+    tree = shapes.tree(shapes.headline())
+    q = torch.empty(128, 32, 128, dtype=torch.bfloat16)
+    p = prepare(schedule(tree, method="cube", model=CostModel.mi355x()), q)
+    stride, maxs = p.abi.slot_stride, p.abi.maxs
+    assert stride == 128 and maxs == 16
+    slots = p.slots.reshape(128, maxs)
+    assert (p.counts == maxs).all()
+    assert torch.equal(slots, torch.arange(128)[:, None] + torch.arange(maxs)[None, :] * stride)
+    assert int(slots.max()) < p.abi.nslot
+    for spec in (shapes.nested_unequal(), shapes.cpu_baseline_shape()):
+        tree = shapes.tree(spec)
+        q = torch.empty(len(tree.paths), 32, 128, dtype=torch.bfloat16)
+        assert prepare(schedule(tree, method="cube", model=CostModel.mi355x()), q).abi.slot_stride == 0

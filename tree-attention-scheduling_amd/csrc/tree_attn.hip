@@ -437,7 +437,9 @@ __global__ __launch_bounds__(64 * NW) void seg_large_kernel(SegParams p) {
 // MERGE_CHUNK slots at once, the 16-byte partial slice (eight fp16 values) and
 // the 8-byte (log-sum-exp, exponent) pair, then merges them online in
 // registers: slots -> (lse, partials) is the only chain of dependent memory
-// round trips; no LDS and no barriers.
+// round trips; no LDS and no barriers.  With an affine slot layout
+// (slot_stride > 0: slot k of request r is r + k * slot_stride, maxs of them)
+// the slots are computed and the partial loads are the first memory access.
 constexpr int MERGE_CHUNK = 16;
 constexpr int MERGE_NT = 128;
 
@@ -446,7 +448,7 @@ __global__ __launch_bounds__(MERGE_NT) void merge_kernel(const u16 *__restrict__
                                                          const int32_t *__restrict__ slots,
                                                          const int32_t *__restrict__ counts,
                                                          const int32_t *__restrict__ reqs, u16 *__restrict__ out,
-                                                         int hq, int maxs) {
+                                                         int hq, int maxs, int slot_stride) {
     constexpr int TPH = D / 8;          // threads per head
     constexpr int MH = MERGE_NT / TPH;  // heads per workgroup
     constexpr float LOG2E = 1.44269504088896341f;
@@ -455,7 +457,7 @@ __global__ __launch_bounds__(MERGE_NT) void merge_kernel(const u16 *__restrict__
     const int hl = tid / TPH, d8 = tid % TPH;
     const int head = blockIdx.y * MH + hl;
     if (head >= hq) return;
-    const int cnt = counts[r];
+    const int cnt = slot_stride > 0 ? maxs : counts[r];
     const int32_t *slr = slots + (size_t)r * maxs;
     const u16 *src = part + (size_t)head * D + 8 * d8;
     const float2 *lse2 = reinterpret_cast<const float2 *>(lse) + head;
@@ -468,7 +470,8 @@ __global__ __launch_bounds__(MERGE_NT) void merge_kernel(const u16 *__restrict__
         u32x4 v[MERGE_CHUNK];
 #pragma unroll
         for (int u = 0; u < MERGE_CHUNK; ++u) {
-            const int sl = slr[min(s0 + u, cnt - 1)];
+            const int k = min(s0 + u, cnt - 1);
+            const int sl = slot_stride > 0 ? r + k * slot_stride : slr[k];
             le[u] = lse2[(size_t)sl * hq];
             v[u] = *(const u32x4 *)(src + sl * srow);
         }
@@ -545,10 +548,11 @@ hipError_t launch_segment(const SegParams &sp, int kind, hipStream_t stream) {
 // nreq requests: reqs[0 .. nreq) when reqs is given, else 0 .. nreq-1
 template <int D, bool FP16>
 hipError_t launch_merge(const void *part, const float *lse, const int32_t *slots, const int32_t *counts,
-                        const int32_t *reqs, void *out, int nreq, int hq, int maxs, hipStream_t stream) {
+                        const int32_t *reqs, void *out, int nreq, int hq, int maxs, hipStream_t stream,
+                        int slot_stride = 0) {
     constexpr int MH = MERGE_NT / (D / 8);
     TA_LAUNCH((merge_kernel<D, FP16>), dim3(nreq, (hq + MH - 1) / MH), dim3(MERGE_NT), stream,
-              static_cast<const u16 *>(part), lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs);
+              static_cast<const u16 *>(part), lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs, slot_stride);
     return hipGetLastError();
 }
 
@@ -658,9 +662,34 @@ int plan_segment(const void *q, const void *kp, const void *vp, int32_t tcap, co
                           plan->maxs, xt ? plan->xtail : nullptr, xt ? plan->xtail_stride : 0, plan->qbase, stream);
 }
 
+// The merge of requests reqs[0 .. n) (reqs == NULL: 0 .. n-1) of a prepared
+// plan into out, with the plan's affine slot layout when it has one.
+int plan_merge(const ta_plan *plan, const int32_t *reqs, int32_t n, void *out, void *stream) {
+    if (!plan->part || !plan->lse || !plan->slots || !plan->counts || n <= 0 || n > plan->nreq) return TA_ERR_ARG;
+    if (plan->dtype != TA_BF16 && plan->dtype != TA_FP16) return TA_ERR_DTYPE;
+    if (plan->maxs <= 0 || plan->hq <= 0 || (plan->d != 32 && plan->d != 64 && plan->d != 128)) return TA_ERR_ARG;
+    if (!aligned16(plan->part) || !aligned16(out) || (reinterpret_cast<uintptr_t>(plan->lse) & 7)) return TA_ERR_ALIGN;
+    // an affine slot layout must stay inside the partial slots
+    if (plan->slot_stride < 0 ||
+        (plan->slot_stride > 0 &&
+         (int64_t)(plan->nreq - 1) + (int64_t)(plan->maxs - 1) * plan->slot_stride >= plan->nslot))
+        return TA_ERR_ARG;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+#define TA_MRG(D, F) \
+    launch_merge<D, F>(plan->part, plan->lse, plan->slots, plan->counts, reqs, out, n, plan->hq, plan->maxs, st, \
+                       plan->slot_stride)
+    return (int)TA_DISPATCH(plan->d, plan->dtype == TA_FP16, TA_MRG);
+#undef TA_MRG
+}
+
 }  // namespace
 
 extern "C" {
+
+int ta_merge_plan(const ta_plan *plan, void *out, void *stream) {
+    if (!plan || !out) return TA_ERR_ARG;
+    return plan_merge(plan, nullptr, plan->nreq, out, stream);
+}
 
 int ta_segment(const void *q, const void *kp, const void *vp, const int32_t *qids, const int32_t *kstart,
                const int32_t *qlen, const int32_t *klen, const int32_t *rowbase, const int32_t *items,
@@ -720,17 +749,8 @@ int ta_attention_matrix(const void *q, const void *kp, const void *vp, int32_t t
         if (int e = plan_segment(q, kp, vp, tcap, plan, TA_TAIL, out, stream)) return e;
     if (plan->n_rest <= 0) return 0;
     // rest == NULL with n_rest == nreq: every request
-    if ((!plan->rest && plan->n_rest != plan->nreq) || !plan->part || !plan->lse || !plan->slots || !plan->counts)
-        return TA_ERR_ARG;
-    if (plan->dtype != TA_BF16 && plan->dtype != TA_FP16) return TA_ERR_DTYPE;
-    if (plan->maxs <= 0 || (plan->d != 32 && plan->d != 64 && plan->d != 128)) return TA_ERR_ARG;
-    if (!aligned16(plan->part) || !aligned16(out) || (reinterpret_cast<uintptr_t>(plan->lse) & 7)) return TA_ERR_ALIGN;
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-#define TA_MRG(D, F) \
-    launch_merge<D, F>(plan->part, plan->lse, plan->slots, plan->counts, plan->rest, out, plan->n_rest, plan->hq, \
-                       plan->maxs, st)
-    return (int)TA_DISPATCH(plan->d, plan->dtype == TA_FP16, TA_MRG);
-#undef TA_MRG
+    if (!plan->rest && plan->n_rest != plan->nreq) return TA_ERR_ARG;
+    return plan_merge(plan, plan->rest, plan->n_rest, out, stream);
 }
 
 int ta_time_next_launch(void *start_event, void *stop_event) {

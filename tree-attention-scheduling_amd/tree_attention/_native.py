@@ -24,7 +24,7 @@ _c_i32 = ctypes.c_int32
 _c_ptr = ctypes.c_void_p
 
 EXPORTS = ("ta_version", "ta_error_string", "ta_segment", "ta_merge", "ta_attention_matrix",
-           "ta_tail_merge", "ta_segment_plan", "ta_decode_append", "ta_time_next_launch")
+           "ta_tail_merge", "ta_segment_plan", "ta_merge_plan", "ta_decode_append", "ta_time_next_launch")
 
 
 class TaPlan(ctypes.Structure):
@@ -36,7 +36,7 @@ class TaPlan(ctypes.Structure):
         ("part", _c_ptr), ("lse", _c_ptr),
         ("njobs", _c_i32), ("maxr", _c_i32), ("maxs", _c_i32), ("nreq", _c_i32), ("nslot", _c_i32),
         ("hq", _c_i32), ("hk", _c_i32), ("d", _c_i32), ("dtype", _c_i32), ("n_rest", _c_i32),
-        ("xtail", _c_ptr), ("xtail_stride", _c_i32), ("qbase", _c_ptr),
+        ("xtail", _c_ptr), ("xtail_stride", _c_i32), ("qbase", _c_ptr), ("slot_stride", _c_i32),
     ]
 
 
@@ -75,6 +75,8 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
                                             _c_ptr, _c_ptr]
         lib.ta_tail_merge.restype = ctypes.c_int
         lib.ta_tail_merge.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_i32, ctypes.POINTER(TaPlan), _c_ptr, _c_ptr]
+        lib.ta_merge_plan.restype = ctypes.c_int
+        lib.ta_merge_plan.argtypes = [ctypes.POINTER(TaPlan), _c_ptr, _c_ptr]
         lib.ta_segment_plan.restype = ctypes.c_int
         lib.ta_segment_plan.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_i32, ctypes.POINTER(TaPlan), _c_i32, _c_ptr]
         lib.ta_decode_append.restype = ctypes.c_int

@@ -419,6 +419,14 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
         slot_array[tail_req] = np.take_along_axis(rows, src, 1)
     items = _build_items(jobs, small_jobs, group, kvheads, tile_rows, tails)
     rest = np.setdiff1d(np.arange(nreq, dtype=np.int32), tail_req.astype(np.int32))
+    # affine slots (slot k of request r is r + k * stride, every request maxs of them):
+    # the merge computes them instead of loading counts and slot lists
+    slot_stride = 0
+    if maxs > 1 and (counts == maxs).all():
+        stride = int(slot_array[0, 1] - slot_array[0, 0])
+        affine = np.arange(nreq)[:, None] + np.arange(maxs)[None, :] * stride
+        if stride > 0 and np.array_equal(slot_array, affine):
+            slot_stride = stride
     # attached segments of each TA_LARGE256 item: count, then (first token, tokens, first job row)
     # (one record per (job, first row), shared by the item of every KV head)
     xstride = 1 + 3 * XTAIL_MAX
@@ -477,6 +485,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     abi.dtype = _DTYPES.get(q.dtype, -1)
     abi.xtail, abi.xtail_stride = (xtail_t.data_ptr(), xstride) if attached else (None, 0)
     abi.qbase = qbase_t.data_ptr()
+    abi.slot_stride = slot_stride
     keyed = {(j + small_jobs, row0): segs for (j, row0), segs in attached.items()}
     return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
                         slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t,
@@ -580,8 +589,7 @@ def merge(prepared, kp=None):
     lib = _native.load()
     with torch.cuda.device(p.out.device):
         stream = torch.cuda.current_stream(p.out.device).cuda_stream
-        rc = lib.ta_merge(abi.part, abi.lse, abi.slots, abi.counts, p.out.data_ptr(), abi.nreq, abi.hq,
-                          abi.d, abi.maxs, abi.dtype, stream)
+        rc = lib.ta_merge_plan(ctypes.byref(abi), p.out.data_ptr(), stream)
     _native.check(rc)
     return p.out
 
