@@ -76,6 +76,27 @@ int tp_attach_tails(int32_t n_large, const int32_t *is256, const int32_t *tiles,
                     int32_t wave_rows, int32_t item_rows, int32_t *item, int32_t *lrow, int32_t *item_job,
                     int32_t *item_row0, int32_t *n_items);
 
+/*
+ * Device metadata of a prepared plan (the backend's prepare(), cf. the
+ * reference's kernels.py:103-141), every int32 section in one buffer:
+ *   qids[njobs*maxr] kstart[njobs] qlen[njobs] klen[njobs] slots[nreq*maxs]
+ *   counts[nreq] rowbase[njobs] rest[n_rest] xtail[n_l256*xstride, only when
+ *   n_att > 0] qbase[njobs] items of kinds TA_SMALL .. TA_TAIL (triples)
+ * as struct ta_plan (tree_attn.h) points into them.  Jobs are in execution
+ * order, small ones (small_jobs of them) first; a job's requests are
+ * req[sum(qlen[0..j)) ..], its tokens [kstart[j], kstart[j] + klen[j]).
+ * Attachments: n_att records of xstride ints for the 256-row items of
+ * (att_job[a], att_row0[a]).  sizes[13]: maxr, maxs, nslot, n_rest,
+ * n_items[5], contiguous (every job's requests span their count), the affine
+ * slot stride (0: none), the buffer length, n_l256.  buf == NULL fills sizes
+ * only.  Returns 0, 1 for invalid arguments (a request outside [0, nreq)),
+ * 2 when buf_len is below the length.
+ */
+int tp_build_metadata(int32_t njobs, int32_t small_jobs, const int32_t *qlen, const int32_t *req,
+                      const int32_t *kstart, const int32_t *klen, int32_t nreq, int32_t group, int32_t kvheads,
+                      int32_t tile_rows, int32_t n_att, const int32_t *att_job, const int32_t *att_row0,
+                      const int32_t *att_rec, int32_t xstride, int32_t *sizes, int32_t *buf, int64_t buf_len);
+
 #ifdef __cplusplus
 }
 #endif

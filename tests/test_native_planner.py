@@ -163,3 +163,42 @@ def test_native_tail_attachment_equals_python(seed):
             assert list(attached) == list(attached_py)
             for key in attached:
                 assert [(id(j), r) for j, r in attached[key]] == [(id(j), r) for j, r in attached_py[key]]
+
+
+def test_native_metadata_equals_numpy():
+    """tp_build_metadata against the numpy builder: same buffer, sections and scalars, over
+    every method on the shape sets, cached decode plans and random trees."""
+    import torch
+    from tree_attention import kernels
+    from tree_attention.kernels import CachedDecodePlan
+
+    captured = []
+    native = kernels._metadata_native
+
+    def both(*args):
+        a, b = native(*args), kernels._metadata_numpy(*args)
+        captured.append((a, b))
+        return a
+
+    kernels._metadata_native = both
+    try:
+        trees = [shapes.tree(shapes.headline()), shapes.tree(shapes.nested_unequal()),
+                 shapes.tree(shapes.cpu_baseline_shape())]
+        trees += [shapes.tree(spec) for _, spec in list(shapes.reference_grid())[::10]]
+        rng = random.Random(5)
+        trees += [_random_tree(rng, rng.randint(2, 30), rng.choice([16, 300])) for _ in range(6)]
+        for tree in trees:
+            q = torch.empty(len(tree.paths), 32, 128, dtype=torch.bfloat16)
+            for method in ("request", "fixed", "cube"):
+                for tile_rows in (256, 128):
+                    kernels.prepare(schedule(tree, method=method, model=CostModel.mi355x()), q, tile_rows)
+            CachedDecodePlan(schedule(tree, method="cube"), q, tree.storage_tokens, 4)
+    finally:
+        kernels._metadata_native = native
+    assert len(captured) > 100
+    for a, b in captured:
+        assert np.array_equal(a["buf"], b["buf"])
+        assert [tuple(s) for s in a["shapes"]] == [tuple(s) for s in b["shapes"]]
+        for key in ("maxr", "maxs", "nslot", "contiguous_q", "slot_stride"):
+            assert a[key] == b[key], key
+        assert np.array_equal(a["qbase"], b["qbase"])

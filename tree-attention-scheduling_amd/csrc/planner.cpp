@@ -445,3 +445,181 @@ extern "C" int tp_attach_tails(int32_t n_large, const int32_t *is256, const int3
     }
     return 0;
 }
+
+// Device metadata of a prepared plan (tree_attention/kernels.py prepare): every
+// int32 section the kernels read, in one buffer, in this order --
+//   qids[njobs*maxr] kids[njobs] qlen[njobs] klen[njobs] slots[nreq*maxs]
+//   counts[nreq] rowbase[njobs] rest[n_rest] xtail[n_l256 * xstride]
+//   qbase[njobs] items of kinds 0 .. 4 (triples)
+// Jobs 0 .. small_jobs-1 are the small ones.  A small job of one request that
+// is its request's only small job is a tail: its items have kind tail and its
+// slot goes last in the request's list (its work item merges the others
+// first); rest is every other request.  Large jobs get row tiles by their row
+// count (64, 128 or 256 rows, at most tile_rows); 256-row items are ordered by
+// KV head, then job, then first row, the others by job, head, first row.
+// Attachments: n_att records of xstride ints (count, then first token, tokens,
+// first job row per segment) for the 256-row items of (att_job, att_row0).
+// sizes (out, 13 ints): maxr, maxs, nslot, n_rest, n_items[5], contiguous_q,
+// slot_stride, total length, n_l256.  buf == NULL: sizes only.  Returns 0, 1
+// for invalid arguments (a request outside [0, nreq)), 2 when buf_len is short.
+extern "C" int tp_build_metadata(int32_t njobs, int32_t small_jobs, const int32_t *qlen, const int32_t *req,
+                                 const int32_t *kstart, const int32_t *klen, int32_t nreq, int32_t group,
+                                 int32_t kvheads, int32_t tile_rows, int32_t n_att, const int32_t *att_job,
+                                 const int32_t *att_row0, const int32_t *att_rec, int32_t xstride, int32_t *sizes,
+                                 int32_t *buf, int64_t buf_len) {
+    if (njobs <= 0 || small_jobs < 0 || small_jobs > njobs || nreq <= 0 || group <= 0 || kvheads <= 0 ||
+        xstride <= 0 || n_att < 0 || !qlen || !req || !kstart || !klen || !sizes || (n_att && (!att_job || !att_row0 || !att_rec)))
+        return 1;
+    std::vector<int64_t> rowbase(njobs);
+    int64_t nslot = 0;
+    int32_t maxr = 0;
+    for (int32_t j = 0; j < njobs; ++j) {
+        if (qlen[j] <= 0) return 1;
+        rowbase[j] = nslot;
+        nslot += qlen[j];
+        maxr = std::max(maxr, qlen[j]);
+    }
+    std::vector<int32_t> counts(nreq, 0);
+    for (int64_t s = 0; s < nslot; ++s) {
+        if (req[s] < 0 || req[s] >= nreq) return 1;
+        ++counts[req[s]];
+    }
+    int32_t maxs = 1;
+    for (int32_t c : counts) maxs = std::max(maxs, c);
+    // tails: single-request small jobs whose request has no other small job
+    std::vector<int32_t> owners(nreq, 0);
+    for (int32_t j = 0; j < small_jobs; ++j)
+        for (int64_t s = rowbase[j]; s < rowbase[j] + qlen[j]; ++s) ++owners[req[s]];
+    std::vector<char> is_tail(njobs, 0), tail_req(nreq, 0);
+    for (int32_t j = 0; j < small_jobs; ++j)
+        if (qlen[j] == 1 && owners[req[rowbase[j]]] == 1) {
+            is_tail[j] = 1;
+            tail_req[req[rowbase[j]]] = 1;
+        }
+    int32_t n_rest = 0;
+    for (int32_t r = 0; r < nreq; ++r) n_rest += !tail_req[r];
+    // row tiles of the large jobs
+    auto kind_of = [&](int64_t rows) {
+        if (rows <= 64 || tile_rows <= 64) return 1;
+        if (rows <= 128 || tile_rows <= 128) return 2;
+        return 3;
+    };
+    static const int tile_of[4] = {0, 64, 128, 256};
+    int64_t n_items[5] = {0, 0, 0, 0, 0};
+    for (int32_t j = 0; j < njobs; ++j) {
+        if (j < small_jobs) {
+            n_items[is_tail[j] ? 4 : 0] += kvheads;
+            continue;
+        }
+        const int64_t rows = (int64_t)qlen[j] * group;
+        const int k = kind_of(rows);
+        n_items[k] += (rows + tile_of[k] - 1) / tile_of[k] * kvheads;
+    }
+    const int64_t n256 = n_items[3];
+    const int64_t total = (int64_t)njobs * maxr + 3 * (int64_t)njobs + (int64_t)nreq * maxs + nreq + njobs + n_rest +
+                          (n_att ? n256 * xstride : 0) + njobs +
+                          3 * (n_items[0] + n_items[1] + n_items[2] + n_items[3] + n_items[4]);
+    // qbase and the span test
+    bool contiguous = true;
+    std::vector<int32_t> qbase(njobs);
+    for (int32_t j = 0; j < njobs; ++j) {
+        const int32_t *r = req + rowbase[j];
+        const int32_t n = qlen[j];
+        contiguous &= r[n - 1] - r[0] + 1 == n;
+        bool consec = true;
+        for (int32_t i = 1; i < n && consec; ++i) consec = r[i] == r[i - 1] + 1;
+        qbase[j] = consec ? r[0] : -1;
+    }
+    // slot lists (positions in job order), the tail slot rotated last
+    std::vector<int64_t> start(nreq + 1, 0);
+    for (int32_t r = 0; r < nreq; ++r) start[r + 1] = start[r] + counts[r];
+    std::vector<int32_t> slot(nslot);
+    {
+        std::vector<int64_t> fill(start.begin(), start.end() - 1);
+        for (int64_t s = 0; s < nslot; ++s) slot[fill[req[s]]++] = (int32_t)s;
+    }
+    for (int32_t r = 0; r < nreq; ++r)
+        if (tail_req[r] && counts[r] > 1) std::rotate(slot.begin() + start[r], slot.begin() + start[r] + 1,
+                                                       slot.begin() + start[r + 1]);
+    int32_t stride = 0;
+    if (maxs > 1) {
+        bool even = true;
+        for (int32_t c : counts) even &= c == maxs;
+        const int32_t st = even ? slot[1] - slot[0] : 0;
+        if (st > 0) {
+            bool affine = true;
+            for (int32_t r = 0; r < nreq && affine; ++r)
+                for (int32_t k = 0; k < maxs && affine; ++k) affine = slot[start[r] + k] == r + k * st;
+            stride = affine ? st : 0;
+        }
+    }
+    const int32_t out_sizes[13] = {maxr, maxs, (int32_t)nslot, n_rest, (int32_t)n_items[0], (int32_t)n_items[1],
+                                   (int32_t)n_items[2], (int32_t)n_items[3], (int32_t)n_items[4], contiguous ? 1 : 0,
+                                   stride, (int32_t)total, (int32_t)n256};
+    std::copy(out_sizes, out_sizes + 13, sizes);
+    if (!buf) return 0;
+    if (buf_len < total) return 2;
+    std::fill(buf, buf + total, 0);
+    int32_t *p = buf;
+    for (int32_t j = 0; j < njobs; ++j)  // qids
+        std::copy(req + rowbase[j], req + rowbase[j] + qlen[j], p + (int64_t)j * maxr);
+    p += (int64_t)njobs * maxr;
+    std::copy(kstart, kstart + njobs, p);
+    p += njobs;
+    std::copy(qlen, qlen + njobs, p);
+    p += njobs;
+    std::copy(klen, klen + njobs, p);
+    p += njobs;
+    for (int32_t r = 0; r < nreq; ++r)  // slots
+        std::copy(slot.begin() + start[r], slot.begin() + start[r + 1], p + (int64_t)r * maxs);
+    p += (int64_t)nreq * maxs;
+    std::copy(counts.begin(), counts.end(), p);
+    p += nreq;
+    for (int32_t j = 0; j < njobs; ++j) p[j] = (int32_t)rowbase[j];
+    p += njobs;
+    for (int32_t r = 0; r < nreq; ++r)  // rest
+        if (!tail_req[r]) *p++ = r;
+    // items, then the attachment records of the 256-row items
+    int32_t *items[5];
+    int32_t *q = p + (n_att ? n256 * xstride : 0) + njobs;
+    for (int k = 0; k < 5; ++k) {
+        items[k] = q;
+        q += 3 * n_items[k];
+    }
+    auto put = [&](int k, int32_t j, int32_t row0, int32_t h) {
+        items[k][0] = j;
+        items[k][1] = row0;
+        items[k][2] = h;
+        items[k] += 3;
+    };
+    for (int32_t j = 0; j < small_jobs; ++j)
+        for (int32_t h = 0; h < kvheads; ++h) put(is_tail[j] ? 4 : 0, j, 0, h);
+    for (int32_t j = small_jobs; j < njobs; ++j) {  // 64- and 128-row kinds: job, head, first row
+        const int64_t rows = (int64_t)qlen[j] * group;
+        const int k = kind_of(rows);
+        if (k == 3) continue;
+        for (int32_t h = 0; h < kvheads; ++h)
+            for (int64_t r0 = 0; r0 < rows; r0 += tile_of[k]) put(k, j, (int32_t)r0, h);
+    }
+    int32_t *big = items[3];
+    for (int32_t h = 0; h < kvheads; ++h)  // 256-row kind: head, job, first row
+        for (int32_t j = small_jobs; j < njobs; ++j) {
+            const int64_t rows = (int64_t)qlen[j] * group;
+            if (kind_of(rows) != 3) continue;
+            for (int64_t r0 = 0; r0 < rows; r0 += 256) put(3, j, (int32_t)r0, h);
+        }
+    if (n_att) {
+        for (int64_t i = 0; i < n256; ++i) {
+            const int32_t j = big[3 * i], r0 = big[3 * i + 1];
+            for (int32_t a = 0; a < n_att; ++a)
+                if (att_job[a] == j && att_row0[a] == r0) {
+                    std::copy(att_rec + (int64_t)a * xstride, att_rec + (int64_t)(a + 1) * xstride,
+                              p + i * xstride);
+                    break;
+                }
+        }
+        p += n256 * xstride;
+    }
+    std::copy(qbase.begin(), qbase.end(), p);
+    return 0;
+}

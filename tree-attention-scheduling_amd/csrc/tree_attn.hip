@@ -40,7 +40,6 @@ namespace {
 
 using namespace ta;
 
-constexpr int NT = 256;         // threads per workgroup (4 waves)
 
 // ------------------------------------------------------- tile staging (LDS)
 // One TTILE-token tile of one KV head: Kt[TTILE][D] (+pad) and Vt[D][TTILE]

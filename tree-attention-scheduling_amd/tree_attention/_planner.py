@@ -3,7 +3,8 @@
 ``grouped_decisions`` hands the tree to ``tp_grouped_plan`` in CSR form and
 returns, per node, whether its parent pushes it (the subset-DP / greedy
 decision of the reference's schedule.py:94-131).  ``attach_tails`` runs the
-tail-attachment step of ``kernels.prepare`` (``tp_attach_tails``).  The
+tail-attachment step of ``kernels.prepare`` (``tp_attach_tails``) and
+``build_metadata`` its device metadata (``tp_build_metadata``).  The
 library is a plain host library (g++), loaded on first use; ``TREE_PLAN_LIB``
 selects another build.
 """
@@ -18,7 +19,7 @@ from pathlib import Path
 import numpy as np
 
 LIB_PATH = Path(__file__).with_name("libtree_plan.so")
-EXPORTS = ("tp_grouped_plan", "tp_attach_tails")
+EXPORTS = ("tp_grouped_plan", "tp_attach_tails", "tp_build_metadata")
 METHODS = {"greedy": 0, "cube": 1}
 
 _lib = None
@@ -48,6 +49,9 @@ def load(required: bool = True):
             lib.tp_attach_tails.restype = ctypes.c_int
             lib.tp_attach_tails.argtypes = ([i32, _p, _p, _p, _p, i32, i32, _p, _p, _p, _p, i32, i32, i32, i32]
                                             + [_p] * 5)
+            lib.tp_build_metadata.restype = ctypes.c_int
+            lib.tp_build_metadata.argtypes = [i32, i32, _p, _p, _p, _p, i32, i32, i32, i32, i32, _p, _p, _p, i32,
+                                              _p, _p, ctypes.c_int64]
             _lib = lib
     return _lib
 
@@ -123,3 +127,21 @@ def attach_tails(large, small, group, is256, large_tiles, small_tiles, fixed, nr
         raise ValueError(f"tp_attach_tails rejected its arguments (code {rc})")
     keys = list(zip(item_job[:n_items[0]].tolist(), item_row0[:n_items[0]].tolist()))
     return item[:ns].tolist(), lrow[:ns].tolist(), keys
+
+
+def build_metadata(qlen, req, kstart, klen, small_jobs, nreq, group, kvheads, tile_rows, att_job, att_row0, att_rec,
+                   xstride):
+    """``tp_build_metadata``: (sizes, one int32 buffer of every metadata section)."""
+    lib = load()
+    one = np.zeros(1, dtype=np.int32)
+    ptr = lambda a: _ptr(a if a.size else one)  # noqa: E731
+    sizes = np.zeros(13, dtype=np.int32)
+    args = (len(qlen), small_jobs, ptr(qlen), ptr(req), ptr(kstart), ptr(klen), nreq, group, kvheads, tile_rows,
+            len(att_job), ptr(att_job), ptr(att_row0), ptr(np.ascontiguousarray(att_rec).reshape(-1)), xstride,
+            _ptr(sizes))
+    if lib.tp_build_metadata(*args, None, 0) != 0:
+        raise ValueError("tp_build_metadata rejected its arguments")
+    buf = np.empty(int(sizes[11]), dtype=np.int32)
+    if lib.tp_build_metadata(*args, _ptr(buf), buf.size) != 0:
+        raise ValueError("tp_build_metadata rejected its arguments")
+    return sizes.tolist(), buf

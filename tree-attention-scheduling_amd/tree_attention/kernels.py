@@ -326,6 +326,125 @@ def _cu_count(device) -> int:
     return 256  # MI355X
 
 
+def _request_error(jobs, nreq):
+    """ValueError naming the first job with a request outside [0, nreq)."""
+    for i, job in enumerate(jobs):
+        for r in job.requests:
+            if not 0 <= r < nreq:
+                return ValueError(f"Job {i} names request {r} outside q's {nreq} requests")
+    return ValueError("a request is outside q's requests")
+
+
+def _metadata_sections(njobs, maxr, nreq, maxs, n_rest, n_l256, attached, xstride, n_items):
+    """Shapes of the int32 metadata sections, in upload order (tp_build_metadata's order)."""
+    return ([(njobs, maxr), (njobs, 1), (njobs,), (njobs,), (nreq, maxs), (nreq,), (njobs,), (n_rest,),
+             (n_l256 if attached else 0, xstride), (njobs,)] + [(3 * n_items[k],) for k in range(_native.TA_NKINDS)])
+
+
+def _metadata_native(jobs, small_jobs, nreq, group, kvheads, tile_rows, attached, xstride):
+    """The metadata sections through the host library (``tp_build_metadata``)."""
+    from . import _planner
+    qlen = np.fromiter((len(j.requests) for j in jobs), dtype=np.int32, count=len(jobs))
+    req = np.fromiter(chain.from_iterable(j.requests for j in jobs), dtype=np.int32, count=int(qlen.sum()))
+    kstart = np.fromiter((j.tokens[0] for j in jobs), dtype=np.int32, count=len(jobs))
+    klen = np.fromiter((len(j.tokens) for j in jobs), dtype=np.int32, count=len(jobs))
+    att_job = np.fromiter((j + small_jobs for j, _ in attached), dtype=np.int32, count=len(attached))
+    att_row0 = np.fromiter((r0 for _, r0 in attached), dtype=np.int32, count=len(attached))
+    att_rec = np.zeros((len(attached), xstride), dtype=np.int32)
+    for i, segs in enumerate(attached.values()):
+        rec = [len(segs)] + [x for job, lrow in segs for x in (job.tokens[0], len(job.tokens), lrow)]
+        att_rec[i, :len(rec)] = rec
+    try:
+        sizes, buf = _planner.build_metadata(qlen, req, kstart, klen, small_jobs, nreq, group, kvheads, tile_rows,
+                                             att_job, att_row0, att_rec, xstride)
+    except ValueError:
+        raise _request_error(jobs, nreq) from None
+    maxr, maxs, nslot, n_rest = sizes[:4]
+    n_items = sizes[4:9]
+    shapes = _metadata_sections(len(jobs), maxr, nreq, maxs, n_rest, sizes[12], attached, xstride, n_items)
+    qbase = buf[-3 * sum(n_items) - len(jobs):len(buf) - 3 * sum(n_items)]
+    return {"buf": buf, "shapes": shapes, "maxr": maxr, "maxs": maxs, "nslot": nslot,
+            "contiguous_q": bool(sizes[9]), "slot_stride": sizes[10], "qbase": qbase}
+
+
+def _metadata_numpy(jobs, small_jobs, nreq, group, kvheads, tile_rows, attached, xstride):
+    """The metadata sections with numpy (the same arrays as ``_metadata_native``)."""
+    njobs = len(jobs)
+    qlen = np.fromiter((len(j.requests) for j in jobs), dtype=np.int32, count=njobs)
+    klen = np.fromiter((len(j.tokens) for j in jobs), dtype=np.int32, count=njobs)
+    kids = np.fromiter((j.tokens[0] for j in jobs), dtype=np.int32, count=njobs).reshape(njobs, 1)
+    ends = np.cumsum(qlen)
+    rowbase = (ends - qlen).astype(np.int32)  # partial slot of each job's first request
+    nslot = int(ends[-1])
+    flat = np.fromiter(chain.from_iterable(j.requests for j in jobs), dtype=np.int64, count=nslot)
+    if flat.size and (flat.min() < 0 or flat.max() >= nreq):
+        raise _request_error(jobs, nreq)
+    maxr = int(qlen.max())
+    local = np.arange(nslot) - np.repeat(rowbase, qlen)  # request's row within its job
+    qids = np.zeros((njobs, maxr), dtype=np.int32)
+    qids[np.repeat(np.arange(njobs), qlen), local] = flat
+    # each request's slots in job order: slot s holds request flat[s]
+    counts = np.bincount(flat, minlength=nreq).astype(np.int32)
+    maxs = max(1, int(counts.max()))
+    order = np.argsort(flat, kind="stable")
+    rank = np.arange(nslot) - np.repeat(np.cumsum(counts) - counts, counts)
+    slot_array = np.zeros((nreq, maxs), dtype=np.int32)
+    slot_array[flat[order], rank] = order
+    tails = _tail_jobs(jobs, small_jobs)
+    tail_list = sorted(tails)
+    tail_req = np.array([jobs[j].requests[0] for j in tail_list], dtype=np.int64)
+    if tail_req.size:
+        # A tail job's slot goes last: its work item merges the request's other
+        # slots first.  Small jobs come first, so it is the request's first slot.
+        rows = slot_array[tail_req]
+        assert (rows[:, 0] == rowbase[tail_list]).all()
+        c = counts[tail_req][:, None]
+        k = np.arange(maxs)[None, :]
+        src = np.where(k < c - 1, k + 1, np.where(k == c - 1, 0, k))
+        slot_array[tail_req] = np.take_along_axis(rows, src, 1)
+    items = _build_items(jobs, small_jobs, group, kvheads, tile_rows, tails)
+    rest = np.setdiff1d(np.arange(nreq, dtype=np.int32), tail_req.astype(np.int32))
+    # affine slots (slot k of request r is r + k * stride, every request maxs of them):
+    # the merge computes them instead of loading counts and slot lists
+    slot_stride = 0
+    if maxs > 1 and (counts == maxs).all():
+        stride = int(slot_array[0, 1] - slot_array[0, 0])
+        affine = np.arange(nreq)[:, None] + np.arange(maxs)[None, :] * stride
+        if stride > 0 and np.array_equal(slot_array, affine):
+            slot_stride = stride
+    # attached segments of each TA_LARGE256 item: count, then (first token, tokens, first job row)
+    # (one record per (job, first row), shared by the item of every KV head)
+    if attached:
+        recs = np.zeros((len(attached), xstride), dtype=np.int32)
+        codes = np.zeros(len(attached), dtype=np.int64)
+        for i, ((j, row0), segs) in enumerate(attached.items()):
+            rec = [len(segs)] + [x for job, lrow in segs for x in (job.tokens[0], len(job.tokens), lrow)]
+            recs[i, :len(rec)] = rec
+            codes[i] = (j + small_jobs) << 32 | row0
+        big = items[_native.TA_LARGE256].reshape(-1, 3).astype(np.int64)
+        item_codes = big[:, 0] << 32 | big[:, 1]
+        order = np.argsort(codes)
+        pos = np.minimum(np.searchsorted(codes[order], item_codes), len(codes) - 1)
+        hit = codes[order][pos] == item_codes
+        xtail = np.zeros((len(big), xstride), dtype=np.int32)
+        xtail[hit] = recs[order[pos[hit]]]
+    else:
+        xtail = np.zeros((0, xstride), dtype=np.int32)
+
+    # first request of each job over consecutive requests, else -1 (kernels.py:23-26, 138)
+    breaks = np.zeros(nslot, dtype=np.int64)
+    breaks[1:] = np.cumsum(np.diff(flat) != 1)  # steps other than +1 up to each slot
+    consecutive = breaks[ends - 1] == breaks[rowbase]
+    qbase = np.where(consecutive, flat[rowbase], -1).astype(np.int32)
+
+    contiguous_q = bool((flat[ends - 1] - flat[rowbase] + 1 == qlen).all())
+    arrays = ([qids, kids, qlen, klen, slot_array, counts, rowbase, rest, xtail, qbase]
+              + [items[k] for k in range(_native.TA_NKINDS)])
+    return {"buf": np.concatenate([a.ravel() for a in arrays]).astype(np.int32, copy=False),
+            "shapes": [a.shape for a in arrays], "maxr": maxr, "maxs": maxs, "nslot": nslot,
+            "contiguous_q": contiguous_q, "slot_stride": slot_stride, "qbase": qbase}
+
+
 def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int | None = None,
             attach_tails: bool = True) -> PreparedPlan:
     """Lower ``plan`` to device metadata and scratch for queries shaped like ``q``.
@@ -383,87 +502,22 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     jobs = small + large
     small_jobs = len(small)
     njobs = len(jobs)
-    qlen = np.fromiter((len(j.requests) for j in jobs), dtype=np.int32, count=njobs)
-    klen = np.fromiter((len(j.tokens) for j in jobs), dtype=np.int32, count=njobs)
-    kids = np.fromiter((j.tokens[0] for j in jobs), dtype=np.int32, count=njobs).reshape(njobs, 1)
-    ends = np.cumsum(qlen)
-    rowbase = (ends - qlen).astype(np.int32)  # partial slot of each job's first request
-    nslot = int(ends[-1])
-    flat = np.fromiter(chain.from_iterable(j.requests for j in jobs), dtype=np.int64, count=nslot)
-    bad = np.flatnonzero((flat < 0) | (flat >= nreq))
-    if bad.size:
-        i = int(np.searchsorted(ends, bad[0], side="right"))
-        raise ValueError(f"Job {i} names request {int(flat[bad[0]])} outside q's {nreq} requests")
-    maxr = int(qlen.max())
-    local = np.arange(nslot) - np.repeat(rowbase, qlen)  # request's row within its job
-    qids = np.zeros((njobs, maxr), dtype=np.int32)
-    qids[np.repeat(np.arange(njobs), qlen), local] = flat
-    # each request's slots in job order: slot s holds request flat[s]
-    counts = np.bincount(flat, minlength=nreq).astype(np.int32)
-    maxs = max(1, int(counts.max()))
-    order = np.argsort(flat, kind="stable")
-    rank = np.arange(nslot) - np.repeat(np.cumsum(counts) - counts, counts)
-    slot_array = np.zeros((nreq, maxs), dtype=np.int32)
-    slot_array[flat[order], rank] = order
-    tails = _tail_jobs(jobs, small_jobs)
-    tail_list = sorted(tails)
-    tail_req = np.array([jobs[j].requests[0] for j in tail_list], dtype=np.int64)
-    if tail_req.size:
-        # A tail job's slot goes last: its work item merges the request's other
-        # slots first.  Small jobs come first, so it is the request's first slot.
-        rows = slot_array[tail_req]
-        assert (rows[:, 0] == rowbase[tail_list]).all()
-        c = counts[tail_req][:, None]
-        k = np.arange(maxs)[None, :]
-        src = np.where(k < c - 1, k + 1, np.where(k == c - 1, 0, k))
-        slot_array[tail_req] = np.take_along_axis(rows, src, 1)
-    items = _build_items(jobs, small_jobs, group, kvheads, tile_rows, tails)
-    rest = np.setdiff1d(np.arange(nreq, dtype=np.int32), tail_req.astype(np.int32))
-    # affine slots (slot k of request r is r + k * stride, every request maxs of them):
-    # the merge computes them instead of loading counts and slot lists
-    slot_stride = 0
-    if maxs > 1 and (counts == maxs).all():
-        stride = int(slot_array[0, 1] - slot_array[0, 0])
-        affine = np.arange(nreq)[:, None] + np.arange(maxs)[None, :] * stride
-        if stride > 0 and np.array_equal(slot_array, affine):
-            slot_stride = stride
-    # attached segments of each TA_LARGE256 item: count, then (first token, tokens, first job row)
-    # (one record per (job, first row), shared by the item of every KV head)
     xstride = 1 + 3 * XTAIL_MAX
-    if attached:
-        recs = np.zeros((len(attached), xstride), dtype=np.int32)
-        codes = np.zeros(len(attached), dtype=np.int64)
-        for i, ((j, row0), segs) in enumerate(attached.items()):
-            rec = [len(segs)] + [x for job, lrow in segs for x in (job.tokens[0], len(job.tokens), lrow)]
-            recs[i, :len(rec)] = rec
-            codes[i] = (j + small_jobs) << 32 | row0
-        big = items[_native.TA_LARGE256].reshape(-1, 3).astype(np.int64)
-        item_codes = big[:, 0] << 32 | big[:, 1]
-        order = np.argsort(codes)
-        pos = np.minimum(np.searchsorted(codes[order], item_codes), len(codes) - 1)
-        hit = codes[order][pos] == item_codes
-        xtail = np.zeros((len(big), xstride), dtype=np.int32)
-        xtail[hit] = recs[order[pos[hit]]]
-    else:
-        xtail = np.zeros((0, xstride), dtype=np.int32)
-
-    # first request of each job over consecutive requests, else -1 (kernels.py:23-26, 138)
-    breaks = np.zeros(nslot, dtype=np.int64)
-    breaks[1:] = np.cumsum(np.diff(flat) != 1)  # steps other than +1 up to each slot
-    consecutive = breaks[ends - 1] == breaks[rowbase]
-    qbase = np.where(consecutive, flat[rowbase], -1).astype(np.int32)
-
-    arrays = ([qids, kids, qlen, klen, slot_array, counts, rowbase, rest, xtail, qbase]
-              + [items[k] for k in sorted(items)])
+    from . import _planner
+    build = _metadata_native if _planner.available() else _metadata_numpy
+    meta = build(jobs, small_jobs, nreq, group, kvheads, tile_rows, attached, xstride)
+    maxr, maxs, nslot, slot_stride = meta["maxr"], meta["maxs"], meta["nslot"], meta["slot_stride"]
     dev = q.device
-    metadata = torch.from_numpy(np.concatenate([a.ravel() for a in arrays])).to(dev)
+    metadata = torch.from_numpy(meta["buf"]).to(dev)
     views, offset = [], 0
-    for array in arrays:
-        views.append(metadata[offset:offset + array.size].view(array.shape))
-        offset += array.size
+    for shape in meta["shapes"]:
+        size = int(np.prod(shape))
+        views.append(metadata[offset:offset + size].view(shape))
+        offset += size
     qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t, rest_t, xtail_t, qbase_t = views[:10]
-    item_views = dict(zip(sorted(items), views[10:]))
-    contiguous_q = bool((flat[ends - 1] - flat[rowbase] + 1 == qlen).all())
+    item_views = dict(zip(range(_native.TA_NKINDS), views[10:]))
+    contiguous_q = meta["contiguous_q"]
+    rest_size = meta["shapes"][7][0]
     # partial rows: fp16 scaled by 2^-e per row; lse holds (log-sum-exp, e) per row
     part = torch.empty((nslot, hq, dim), device=dev, dtype=torch.float16)
     lse = torch.empty((nslot, hq, 2), device=dev, dtype=torch.float32)
@@ -477,8 +531,8 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
         abi.items[kind] = view.data_ptr() if view.numel() else None
         abi.n_items[kind] = view.numel() // 3
     # rest = every request: the merge takes requests 0..nreq-1 directly (one dependent load less)
-    every = rest.size == nreq
-    abi.rest, abi.n_rest = (rest_t.data_ptr() if rest.size and not every else None), int(rest.size)
+    every = rest_size == nreq
+    abi.rest, abi.n_rest = (rest_t.data_ptr() if rest_size and not every else None), int(rest_size)
     abi.part, abi.lse = part.data_ptr(), lse.data_ptr()
     abi.njobs, abi.maxr, abi.maxs, abi.nreq, abi.nslot = njobs, maxr, maxs, nreq, nslot
     abi.hq, abi.hk, abi.d = hq, kvheads, dim
@@ -490,7 +544,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
                         slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t,
                         keyed, xtail_t if attached else None, plan,
-                        {"tile_rows": tile_rows, "fixed_from": fixed_from}, None, qbase.tolist())
+                        {"tile_rows": tile_rows, "fixed_from": fixed_from}, None, meta["qbase"].tolist())
 
 
 def pack_kv(k: torch.Tensor, v: torch.Tensor):
