@@ -27,6 +27,7 @@ Internal layout (the build's own; only ``out`` is contractual):
 from __future__ import annotations
 
 import ctypes
+import math
 from dataclasses import dataclass, field
 from itertools import chain
 
@@ -509,11 +510,9 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     maxr, maxs, nslot, slot_stride = meta["maxr"], meta["maxs"], meta["nslot"], meta["slot_stride"]
     dev = q.device
     metadata = torch.from_numpy(meta["buf"]).to(dev)
-    views, offset = [], 0
-    for shape in meta["shapes"]:
-        size = int(np.prod(shape))
-        views.append(metadata[offset:offset + size].view(shape))
-        offset += size
+    sizes = [math.prod(shape) for shape in meta["shapes"]]
+    views = [part if len(shape) == 1 else part.view(shape)
+             for part, shape in zip(metadata[:sum(sizes)].split(sizes), meta["shapes"])]
     qids_t, kids_t, qlen_t, klen_t, slots_t, counts_t, rowbase_t, rest_t, xtail_t, qbase_t = views[:10]
     item_views = dict(zip(range(_native.TA_NKINDS), views[10:]))
     contiguous_q = meta["contiguous_q"]
