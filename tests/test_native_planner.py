@@ -68,8 +68,8 @@ def test_invalid_arguments_are_rejected():
     p = one.ctypes.data_as(ctypes.c_void_p)
     assert lib.tp_grouped_plan(2, 1, *([p] * 11)) == 1  # unknown method
     iparams = np.array([16, 128, 512, 64, 30, 8, 128], dtype=np.int64)  # 30 % 8 != 0
-    args = [p] * 11
-    args[9] = iparams.ctypes.data_as(ctypes.c_void_p)
+    args = [p] * 11  # parent .. fparams, iparams (index 8), pushed, total
+    args[8] = iparams.ctypes.data_as(ctypes.c_void_p)
     assert lib.tp_grouped_plan(1, 1, *args) == 1
 
 
