@@ -207,42 +207,54 @@ def main():
                                 max(POOLS, args.steps // 4), max(2, args.warmup // 2))
 
     # CPU leg after the GPU timing (the GPU would idle through it and start the timing cold)
-    cpu = cpu_baseline(q, k, v, tree, plan, args.cpu_budget_s)
+    cpu = cpu_baseline(q, k, v, tree, plan, args.cpu_budget_s, args.seed)
 
-    # ---- roofline of the dominant kernel
+    # ---- roofline of the dominant kernel: both floors from its algorithmic work, the larger binds
     jobs = prepared.jobs
     small_rows = HQ // HK
     small_tokens = sum(len(j.tokens) for j in jobs if len(j.requests) * small_rows <= 16)
     tail_jobs = sorted({j for j, _, _ in prepared.items[_native.TA_TAIL].view(-1, 3).tolist()})
     tail_requests = [jobs[j].requests[0] for j in tail_jobs]
     counts = prepared.counts.tolist()
+    large_jobs = [j for j in jobs if len(j.requests) * small_rows > 16]
+    attached = [t for segs in prepared.attached.values() for t, _ in segs]
     # the large kernels' work: their jobs, plus the private segments attached to their items
-    large_flops = (sum(4 * len(j.requests) * HQ * len(j.tokens) * D for j in jobs
-                       if len(j.requests) * small_rows > 16)
-                   + sum(4 * HQ * len(t.tokens) * D for segs in prepared.attached.values() for t, _ in segs))
+    large_flops = (sum(4 * len(j.requests) * HQ * len(j.tokens) * D for j in large_jobs)
+                   + sum(4 * HQ * len(t.tokens) * D for t in attached))
+    # their physical KV: every token of a large job or attached segment, read once per KV head
+    large_kv_bytes = physical_kv_bytes(sum(len(j.tokens) for j in large_jobs) + sum(len(t.tokens) for t in attached))
+    partial_row = HQ * (2 * D + 8)  # one slot: fp16 row per query head + (lse, exponent) fp32 pair
     dominant = max(kernel_us, key=kernel_us.get)
     traffic = _pmc_traffic(dominant)
+    t_s = kernel_us[dominant] * 1e-6
     if dominant.startswith("segment_large"):
-        achieved = large_flops / (kernel_us[dominant] * 1e-6) / 1e12
-        roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1),
-                    "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
-                    "algorithmic": f"{large_flops} FLOP per launch (4 x rows x tokens x D over the large jobs "
-                                   f"and their attached private segments)"}
-    else:
-        if dominant == "segment_small":
-            nbytes = physical_kv_bytes(small_tokens)
-        elif dominant == "segment_tail_merge":
-            # tail KV, the other partial slots of each tail request (o and lse), the output rows
-            nbytes = (physical_kv_bytes(sum(len(jobs[j].tokens) for j in tail_jobs))
-                      + sum(counts[r] - 1 for r in tail_requests) * HQ * (D + 1) * 4
-                      + len(tail_requests) * HQ * D * 2)
-        else:
-            nbytes = sum(counts) * HQ * (D + 1) * 4 + len(counts) * HQ * D * 2
-        achieved = nbytes / (kernel_us[dominant] * 1e-6) / 1e9
-        roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                    "algorithmic": f"{nbytes} B per launch"}
+        nbytes, flops = large_kv_bytes, large_flops
+        work = (f"{large_kv_bytes} B of physical KV (K and V of every token of the large jobs and their "
+                f"attached private segments, per KV head) and {large_flops} FLOP (4 x rows x tokens x D) per launch")
+    elif dominant == "segment_small":
+        nbytes, flops = physical_kv_bytes(small_tokens), 0
+        work = f"{nbytes} B of physical KV per launch"
+    elif dominant == "segment_tail_merge":
+        # tail KV, the other partial slots of each tail request, the output rows
+        nbytes = (physical_kv_bytes(sum(len(jobs[j].tokens) for j in tail_jobs))
+                  + sum(counts[r] - 1 for r in tail_requests) * partial_row + len(tail_requests) * HQ * D * 2)
+        flops = 0
+        work = f"{nbytes} B per launch (tail KV, partial slots, output)"
+    else:  # merge: every slot's partial row and (lse, exponent), then the output row
+        nbytes, flops = sum(counts) * partial_row + len(counts) * HQ * D * 2, 0
+        work = f"{nbytes} B per launch (partial slots and output)"
+    hbm_floor_s = nbytes / (HBM_PEAK_GBS * 1e9)
+    mfma_floor_s = flops / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+    hbm = {"achieved": round(nbytes / t_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(hbm_floor_s / t_s, 4), "floor_us": round(hbm_floor_s * 1e6, 3)}
+    mfma = {"achieved": round(flops / t_s / 1e12, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(mfma_floor_s / t_s, 4), "floor_us": round(mfma_floor_s * 1e6, 3)}
+    bound, other = ("hbm", mfma) if hbm_floor_s >= mfma_floor_s else ("mfma", hbm)
+    main = hbm if bound == "hbm" else mfma
+    roofline = {"kernel": dominant, "bound": bound, "achieved": main["achieved"], "peak": main["peak"],
+                "unit": main["unit"], "frac": main["frac"], "traffic": traffic, "kernel_us": round(kernel_us[dominant], 3),
+                "floor_us": main["floor_us"], "algorithmic": work,
+                ("mfma" if bound == "hbm" else "hbm"): other}
 
     kv_bytes = physical_kv_bytes(T)
     value = kv_bytes / (us_per_layer * 1e-6) / 1e9
@@ -295,30 +307,66 @@ def parity_rel_l2(q, k, v, tree, gpu_out):
     return relative_l2(gpu_out, request_attention(q.float(), k.float(), v.float(), tree))
 
 
-def cpu_baseline(q, k, v, tree, plan, budget_s):
-    """CPU leg: the FP32 oracle's plan-driven ``segmented_attention``
-    (reference.py:16-33) on the host cores, on the same layer and plan
-    (median of up to 5 runs within ``budget_s``)."""
-    import torch
-    from oracle.attention_oracle import segmented_attention
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    qf, kf, vf = q.float(), k.float(), v.float()
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), else the architecture."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _time_cpu(fn, warmup, iters, budget_s):
+    for _ in range(warmup):
+        fn()
     times = []
     t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 1:
+    while len(times) < iters and (time.perf_counter() < t_end or len(times) < 1):
         t0 = time.perf_counter()
-        segmented_attention(qf, kf, vf, plan)
+        fn()
         times.append(time.perf_counter() - t0)
-        if len(times) >= 5:
-            break
-    us = statistics.median(times) * 1e6
-    gbs = physical_kv_bytes(tree.storage_tokens) / (us * 1e-6) / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "us_per_layer": round(us, 1), "cores": cores,
-           "threads": torch.get_num_threads(), "kind": "port",
-           "sample": f"{len(times)} full layer(s) of the same workload and plan through the oracle's "
-                     f"segmented_attention in fp32 (median)",
-           "cpu": platform.processor() or platform.machine()}
+    return statistics.median(times) * 1e6, len(times)
+
+
+def cpu_baseline(q, k, v, tree, plan, budget_s, seed):
+    """CPU leg: the FP32 oracle's plan-driven ``segmented_attention``
+    (reference.py:16-33) on the host cores.
+
+    ``value``: the CPU-baseline configuration (8 requests, 1024-token shared
+    root + 64 private tokens each, fp32 N(0,1) Q/K/V from ``seed``, per-request
+    plan; 2 warm-ups, then the median of 20 runs).  ``same_layer``: the timed
+    GPU layer and plan in fp32 (median of up to 5 runs within ``budget_s``).
+    Both in physical-KV GB/s (bf16 K and V bytes of the tree, the metric's
+    denominator)."""
+    import torch
+    from oracle.attention_oracle import request_attention, segmented_attention
+    from tree_attention import schedule, shapes
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    small = shapes.tree(shapes.cpu_baseline_shape())
+    g = torch.Generator().manual_seed(seed)
+    q1 = torch.randn(len(small.paths), HQ, D, generator=g)
+    k1 = torch.randn(small.storage_tokens, HK, D, generator=g)
+    v1 = torch.randn(small.storage_tokens, HK, D, generator=g)
+    plan1 = schedule(small, HQ, HK, D, "request")
+    a = segmented_attention(q1, k1, v1, plan1)
+    b = request_attention(q1, k1, v1, small)  # cross-check of the timed function
+    if not torch.allclose(a, b, atol=2e-5, rtol=2e-5):
+        raise RuntimeError("oracle segmented_attention disagrees with request_attention on the CPU-baseline shape")
+    us1, n1 = _time_cpu(lambda: segmented_attention(q1, k1, v1, plan1), 2, 20, budget_s)
+    qf, kf, vf = q.float(), k.float(), v.float()
+    us2, n2 = _time_cpu(lambda: segmented_attention(qf, kf, vf, plan), 0, 5, budget_s)
+    gb = lambda tokens, us: round(physical_kv_bytes(tokens) / (us * 1e-6) / 1e9, 3)  # noqa: E731
+    return {"value": gb(small.storage_tokens, us1), "unit": "GB/s", "us_per_layer": round(us1, 1),
+            "cores": cores, "threads": torch.get_num_threads(), "kind": "port",
+            "sample": (f"CPU-baseline configuration: 8 requests x (1024 shared + 64 private) tokens, 32Q/8KV, "
+                       f"d=128, fp32, per-request plan ({len(plan1.jobs)} jobs) through the oracle's "
+                       f"segmented_attention; median of {n1} runs after 2 warm-ups"),
+            "cpu": cpu_model(),
+            "same_layer": {"value": gb(tree.storage_tokens, us2), "unit": "GB/s", "us_per_layer": round(us2, 1),
+                           "sample": f"the timed 128 x 8192 layer and plan in fp32, median of {n2} run(s)"}}
 
 
 if __name__ == "__main__":

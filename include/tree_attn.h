@@ -168,8 +168,11 @@ int ta_segment_plan(const void *q, const void *kp, const void *vp, int32_t tcap,
  * row shared by all requests); Q and K are rotated (rotate-half RoPE, each
  * multiply and the add rounded to dtype as the eager ops are), Q is written to
  * q_out [nreq, hq, d], K to kp[h, :, slots[r]] and V to vp[h, slots[r], :]
- * (pools [hk, d, tcap] / [hk, tcap, d]); a slot outside [0, tcap) writes
- * nothing.  No counterpart kernel in the reference. */
+ * (pools [hk, d, tcap] / [hk, tcap, d]).  A slot outside [0, tcap) writes
+ * nothing: a guard only, since the library cannot raise from the device; the
+ * Python wrapper range-checks slots given as host data and raises ValueError,
+ * as the eager index_copy_ of the reference adapter does.  No counterpart
+ * kernel in the reference. */
 int ta_decode_append(const void *q, const void *k, const void *v, const void *cos, const void *sin,
                      int32_t cs_stride, const int32_t *slots, void *kp, void *vp, void *q_out,
                      int32_t nreq, int32_t hq, int32_t hk, int32_t d, int32_t tcap, int32_t dtype,

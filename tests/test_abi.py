@@ -71,3 +71,23 @@ def test_xtail_record_layout_matches_header():
     header = (Path(__file__).resolve().parents[1] / "include" / "tree_attn.h").read_text()
     assert int(re.search(r"#define TA_XTAIL_MAX (\d+)", header).group(1)) == kernels.XTAIL_MAX
     assert "#define TA_XTAIL_STRIDE (1 + 3 * TA_XTAIL_MAX)" in header
+
+
+def test_decode_append_rejects_host_slots_outside_the_pool():
+    """Slots given as host data are range-checked before any launch (the eager
+    index_copy_ of the reference adapter, qwen.py:89-90, raises for them too)."""
+    import torch
+    from tree_attention.kernels import decode_append
+    nreq, hq, hk, d, tcap = 3, 8, 2, 32, 16
+    q = torch.zeros(nreq, 1, hq, d, dtype=torch.bfloat16)
+    k = torch.zeros(nreq, 1, hk, d, dtype=torch.bfloat16)
+    v = torch.zeros(nreq, 1, hk, d, dtype=torch.bfloat16)
+    cos = torch.ones(nreq, 1, d, dtype=torch.bfloat16)
+    sin = torch.zeros(nreq, 1, d, dtype=torch.bfloat16)
+    kp = torch.zeros(hk, d, tcap, dtype=torch.bfloat16)
+    vp = torch.zeros(hk, tcap, d, dtype=torch.bfloat16)
+    for bad in ([0, 5, tcap], [-1, 2, 3], torch.tensor([1, 2, tcap + 7])):
+        with pytest.raises(ValueError, match="pool capacity"):
+            decode_append(q, k, v, cos, sin, bad, kp, vp)
+    with pytest.raises(ValueError, match="one pool position per request"):
+        decode_append(q, k, v, cos, sin, [0, 1], kp, vp)

@@ -95,6 +95,22 @@ def test_npu_correctness_logical_jobs():
         assert len(plan.jobs) == row["logical_jobs"], row
 
 
+def test_fixtures_pin_the_current_fit():
+    """The FITTED plans of plan_fixtures.json were made with the parameters in
+    mi355x_cost_model.json: a re-fit without regenerating the fixtures
+    (tests/golden/make_plan_fixtures.py) fails here."""
+    data = _load("plan_fixtures.json")
+    fitted = CostModel.mi355x().__dict__
+    assert data["fitted"] == fitted
+    fitted_plans = [(case["name"], p) for case in data["cases"] for p in case["plans"] if p["model"] == fitted]
+    names = {name for name, _ in fitted_plans}
+    # the configurations bench.py and the model tests run are among them
+    assert {"wide_long", "cpu_baseline", "nested_unequal", "no_share_long"} <= names
+    assert sum(name.startswith("grid_") for name in names) == 81
+    head = {p["method"]: p for name, p in fitted_plans if name == "wide_long"}
+    assert head["cube"]["estimated_us"] == 44.53956174077478
+
+
 @IMPLS
 def test_plans_match_reference_implementation(native):
     """Exact job tuples, job order and estimated_us, including non-default parameters."""

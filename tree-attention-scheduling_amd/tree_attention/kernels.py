@@ -659,6 +659,12 @@ def decode_append(q, k, v, cos, sin, slots, kp, vp, q_out=None):
     step's pool positions, ``kp [HK, D, T]`` / ``vp [HK, T, D]``.  Returns the
     rotated Q ``[R, HQ, D]`` (``q_out`` if given).  The results are
     bit-identical to the eager ops in bf16 and fp16.
+
+    ``slots`` given as host data (a sequence or a CPU tensor) are range-checked
+    here: a position outside ``[0, T)`` raises ``ValueError``, as the eager
+    ``index_copy_`` does.  Slots already on the GPU are not read back (that
+    would synchronise the host); the kernel then skips a position outside the
+    pool, writing nothing for it.
     """
     nreq = q.shape[0]
     d = q.shape[-1]
@@ -675,9 +681,13 @@ def decode_append(q, k, v, cos, sin, slots, kp, vp, q_out=None):
         raise ValueError("cos and sin need D values per request or one row for all")
     cs_stride = d if cos2.shape[0] == nreq else 0
     q2, k2, v2, cos2, sin2 = (t.contiguous() for t in (q2, k2, v2, cos2, sin2))
-    slots = slots.to(device=q.device, dtype=torch.int32).contiguous()
+    if not isinstance(slots, torch.Tensor):
+        slots = torch.tensor(list(slots), dtype=torch.int64)
     if slots.numel() != nreq:
         raise ValueError("slots needs one pool position per request")
+    if not slots.is_cuda and nreq and not (0 <= int(slots.min()) and int(slots.max()) < kp.shape[2]):
+        raise ValueError(f"slots must lie in [0, {kp.shape[2]}) (the pool capacity)")
+    slots = slots.to(device=q.device, dtype=torch.int32).contiguous()
     if q_out is None:
         q_out = torch.empty((nreq, hq, d), device=q.device, dtype=q.dtype)
     lib = _native.load()

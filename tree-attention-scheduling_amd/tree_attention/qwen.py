@@ -226,7 +226,11 @@ class SharedKVDecoder:
         if len(token_ids) != len(self.sequences):
             raise ValueError("step needs exactly one token per request")
         rope_pos = torch.tensor([[len(s)] for s in self.sequences], device=self.device)
-        slots = torch.tensor(self._append(token_ids), device=self.device, dtype=torch.int32)
+        positions = self._append(token_ids)
+        cap = self.pools[0][0].shape[2]
+        if not all(0 <= p < cap for p in positions):  # host data: the fused kernel would skip them silently
+            raise ValueError(f"pool slots {positions} outside the pool capacity {cap}")
+        slots = torch.tensor(positions, device=self.device, dtype=torch.int32)
         prepared = self._prepare_plan()
         pools = self.pools
         nreq = len(token_ids)
