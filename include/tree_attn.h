@@ -62,6 +62,13 @@ extern "C" {
 #define TA_ERR_ARG 1001      /* null pointer, bad size or unsupported shape */
 #define TA_ERR_ALIGN 1002    /* q / kp / vp / part / out not 16-byte aligned, lse not 8-byte */
 #define TA_ERR_DTYPE 1003    /* dtype not TA_BF16 / TA_FP16 */
+#define TA_ERR_SCRATCH 1004  /* ta_attention_matrix_noalloc: partials beyond TA_NOALLOC_SCRATCH_BYTES */
+
+/* Device memory of ta_attention_matrix_noalloc's partials, per GPU: the plan's
+ * nslot * hq * d fp16 partial rows, rounded up to 256 bytes, plus
+ * nslot * hq (lse, exponent) fp32 pairs must fit (32 MiB: e.g. 4,096 slots of
+ * 32 query heads at d = 128; the 128 x 8192 headline layer needs 17.3 MB). */
+#define TA_NOALLOC_SCRATCH_BYTES (32u << 20)
 
 /* Everything one attention_matrix call needs besides q, kp, vp and out.
  * Built once per plan by the host (kernels.py:103-141 `prepare`). */
@@ -137,6 +144,22 @@ int ta_merge(const void *part, const float *lse, const int32_t *slots,
  * requests. */
 int ta_attention_matrix(const void *q, const void *kp, const void *vp,
                         int32_t tcap, const ta_plan *plan, void *out, void *stream);
+
+/* ta_attention_matrix without caller-provided partial buffers.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  The same launches and results as ta_attention_matrix, but
+ * the partial rows and log-sum-exp values live in a fixed array of the library
+ * (TA_NOALLOC_SCRATCH_BYTES; each GPU the library runs on holds one until the
+ * process ends); plan->part and plan->lse are ignored and may be NULL.  The
+ * call allocates nothing; a plan whose partials do not fit returns
+ * TA_ERR_SCRATCH before any launch.  Every call on one GPU shares that GPU's
+ * array, which keeps the last call's contents (each call writes every slot it
+ * reads): calls that overlap on one GPU -- other streams, other host threads --
+ * race; calls ordered on one stream do not.  The current device must be the
+ * stream's device (TA_ERR_ARG otherwise). */
+int ta_attention_matrix_noalloc(const void *q, const void *kp, const void *vp,
+                                int32_t tcap, const ta_plan *plan, void *out, void *stream);
 
 /* The TA_TAIL launch of ta_attention_matrix on its own: each work item attends
  * its request's tail job and merges the request's other partial slots (written

@@ -1,0 +1,78 @@
+"""ta_attention_matrix_noalloc, the entry point that allocates nothing, against ta_attention_matrix.
+
+Both run the same kernels on the same plan; the no-allocation variant keeps
+the partials in the library's fixed per-GPU array instead of the plan's
+buffers, so the outputs must be bit-identical.  Two calls in a row, the
+second on a smaller layer, plus a third repeating the first: each call's
+result must not depend on what the previous one left in the array.
+"""
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from tree_attention import CostModel, _native, schedule, shapes
+from tree_attention.kernels import pack_kv, prepare
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+def _layer(spec, model, seed, device):
+    tree = shapes.tree(spec)
+    g = torch.Generator().manual_seed(seed)
+    t = -(-tree.storage_tokens // 8) * 8
+    q = torch.randn(len(tree.paths), 32, 128, generator=g).bfloat16().to(device)
+    k = torch.randn(t, 8, 128, generator=g).bfloat16().to(device)
+    v = torch.randn(t, 8, 128, generator=g).bfloat16().to(device)
+    kp, vp = pack_kv(k, v)
+    prepared = prepare(schedule(tree, 32, 8, 128, "cube", model), q)
+    return q, kp, vp, prepared
+
+
+def _call(name, q, kp, vp, abi, out):
+    lib = _native.load()
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        return getattr(lib, name)(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), kp.shape[2], ctypes.byref(abi),
+                                  out.data_ptr(), stream)
+
+
+def test_noalloc_equals_attention_matrix(device):
+    layers = [("headline 128 x 8192", shapes.headline(), CostModel.mi355x(), 101),
+              ("wide 32 x 2112 (smaller)", shapes.benchmark_cases()["wide"], CostModel(), 7),
+              ("headline again", shapes.headline(), CostModel.mi355x(), 5)]
+    for name, spec, model, seed in layers:
+        q, kp, vp, prepared = _layer(spec, model, seed, device)
+        abi = prepared.abi
+        need = abi.nslot * abi.hq * abi.d * 2 + abi.nslot * abi.hq * 8
+        say("noalloc", name, "slots", abi.nslot, "partial bytes", need)
+        assert need <= _native.NOALLOC_SCRATCH_BYTES
+        # the variant ignores the plan's partial buffers
+        bare = _native.TaPlan.from_buffer_copy(abi)
+        bare.part, bare.lse = None, None
+        a = torch.empty_like(q)
+        b = torch.full_like(q, float("nan"))
+        assert _call("ta_attention_matrix", q, kp, vp, abi, a) == 0
+        assert _call("ta_attention_matrix_noalloc", q, kp, vp, bare, b) == 0
+        torch.cuda.synchronize()
+        assert torch.isfinite(b.float()).all(), name
+        assert torch.equal(a, b), name
+        if name.startswith("wide"):
+            assert abi.n_items[_native.TA_TAIL] > 0  # the fused tail-merge kernel ran on the array too
+
+
+def test_noalloc_rejects_plans_beyond_its_array(device):
+    q, kp, vp, prepared = _layer(shapes.benchmark_cases()["wide"], CostModel(), 3, device)
+    big = _native.TaPlan.from_buffer_copy(prepared.abi)
+    big.nslot = _native.NOALLOC_SCRATCH_BYTES // (big.hq * big.d * 2) + 1
+    out = torch.zeros_like(q)
+    assert _call("ta_attention_matrix_noalloc", q, kp, vp, big, out) == _native.TA_ERR_SCRATCH
+    torch.cuda.synchronize()
+    assert not out.any()  # nothing was launched
+    assert b"TA_NOALLOC_SCRATCH_BYTES" in _native.load().ta_error_string(_native.TA_ERR_SCRATCH)

@@ -33,6 +33,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "ta_common.h"
 #include "tree_attn.h"
 
@@ -585,6 +587,8 @@ const char *ta_error_string(int code) {
         case TA_ERR_ARG: return "tree_attn: invalid argument (null pointer, size or unsupported shape)";
         case TA_ERR_ALIGN: return "tree_attn: q/kp/vp/part/out must be 16-byte aligned, lse 8-byte aligned";
         case TA_ERR_DTYPE: return "tree_attn: dtype must be TA_BF16 or TA_FP16";
+        case TA_ERR_SCRATCH:
+            return "tree_attn: the plan's partials exceed TA_NOALLOC_SCRATCH_BYTES (use ta_attention_matrix)";
         default: return hipGetErrorString((hipError_t)code);
     }
 }
@@ -722,8 +726,18 @@ int ta_tail_merge(const void *q, const void *kp, const void *vp, int32_t tcap, c
     return plan_segment(q, kp, vp, tcap, plan, TA_TAIL, out, stream);
 }
 
-int ta_attention_matrix(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan,
-                        void *out, void *stream) {
+}  // extern "C"
+
+// Partial rows and log-sum-exp values of ta_attention_matrix_noalloc.  Each
+// GPU the library runs on holds its own copy until the process ends.  In host
+// code the name is a stand-in, not a device address: kernels get the address
+// hipGetSymbolAddress returns for the current device (noalloc_scratch).
+static __device__ __align__(256) unsigned char scratch[TA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+int attention_layer(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan, void *out,
+                    void *stream) {
     if (!plan || !out) return TA_ERR_ARG;
 #ifdef TA_LEGACY_LARGE
     const bool fused = false;
@@ -750,6 +764,61 @@ int ta_attention_matrix(const void *q, const void *kp, const void *vp, int32_t t
     // rest == NULL with n_rest == nreq: every request
     if (!plan->rest && plan->n_rest != plan->nreq) return TA_ERR_ARG;
     return plan_merge(plan, plan->rest, plan->n_rest, out, stream);
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+unsigned char *g_scratch[kMaxDevices];  // per device: the device address of `scratch`
+
+// The address of `scratch` on the current device, looked up once per device
+// (with that device current) and kept.
+int noalloc_scratch(unsigned char **ptr) {
+    int dev = -1;
+    if (hipError_t e = hipGetDevice(&dev)) return (int)e;
+    if (dev < 0 || dev >= kMaxDevices) return TA_ERR_ARG;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) return (int)e;
+        if (!p) return TA_ERR_ARG;
+        g_scratch[dev] = static_cast<unsigned char *>(p);
+    }
+    *ptr = g_scratch[dev];
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ta_attention_matrix(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan,
+                        void *out, void *stream) {
+    return attention_layer(q, kp, vp, tcap, plan, out, stream);
+}
+
+int ta_attention_matrix_noalloc(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan,
+                                void *out, void *stream) {
+    if (!plan || !out) return TA_ERR_ARG;
+    if (plan->nslot <= 0 || plan->hq <= 0 || plan->d <= 0) return TA_ERR_ARG;
+    // partial rows (fp16) first, then the (lse, exponent) pairs at a 256-byte boundary
+    const uint64_t part_bytes = (uint64_t)plan->nslot * (uint64_t)plan->hq * (uint64_t)plan->d * 2u;
+    const uint64_t lse_offset = (part_bytes + 255u) & ~(uint64_t)255u;
+    const uint64_t lse_bytes = (uint64_t)plan->nslot * (uint64_t)plan->hq * 2u * sizeof(float);
+    if (lse_offset + lse_bytes > (uint64_t)TA_NOALLOC_SCRATCH_BYTES) return TA_ERR_SCRATCH;
+    unsigned char *base = nullptr;
+    if (int e = noalloc_scratch(&base)) return e;
+    if (stream) {  // the scratch address belongs to the current device: the stream must be on it
+        int cur = -1, sdev = -1;
+        if (hipError_t e = hipGetDevice(&cur)) return (int)e;
+        if (hipError_t e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev)) return (int)e;
+        if (cur != sdev) return TA_ERR_ARG;
+    }
+    // every partial slot the merge reads is written by a segment launch of the
+    // same call first, so nothing in the array needs clearing
+    ta_plan local = *plan;
+    local.part = base;
+    local.lse = reinterpret_cast<float *>(base + lse_offset);
+    return attention_layer(q, kp, vp, tcap, &local, out, stream);
 }
 
 int ta_time_next_launch(void *start_event, void *stop_event) {

@@ -18,13 +18,15 @@ LIB_PATH = Path(__file__).with_name("libtree_attn.so")
 TA_BF16, TA_FP16 = 0, 1
 TA_SMALL, TA_LARGE64, TA_LARGE128, TA_LARGE256, TA_TAIL = 0, 1, 2, 3, 4
 TA_NKINDS = 5
+TA_ERR_SCRATCH = 1004
+NOALLOC_SCRATCH_BYTES = 32 << 20  # TA_NOALLOC_SCRATCH_BYTES
 KIND_ROWS = {TA_LARGE64: 64, TA_LARGE128: 128, TA_LARGE256: 256}
 
 _c_i32 = ctypes.c_int32
 _c_ptr = ctypes.c_void_p
 
 EXPORTS = ("ta_version", "ta_error_string", "ta_segment", "ta_merge", "ta_attention_matrix",
-           "ta_tail_merge", "ta_segment_plan", "ta_merge_plan", "ta_decode_append", "ta_time_next_launch")
+           "ta_attention_matrix_noalloc", "ta_tail_merge", "ta_segment_plan", "ta_merge_plan", "ta_decode_append", "ta_time_next_launch")
 
 
 class TaPlan(ctypes.Structure):
@@ -73,6 +75,9 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         lib.ta_attention_matrix.restype = ctypes.c_int
         lib.ta_attention_matrix.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_i32, ctypes.POINTER(TaPlan),
                                             _c_ptr, _c_ptr]
+        lib.ta_attention_matrix_noalloc.restype = ctypes.c_int
+        lib.ta_attention_matrix_noalloc.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_i32, ctypes.POINTER(TaPlan),
+                                                    _c_ptr, _c_ptr]
         lib.ta_tail_merge.restype = ctypes.c_int
         lib.ta_tail_merge.argtypes = [_c_ptr, _c_ptr, _c_ptr, _c_i32, ctypes.POINTER(TaPlan), _c_ptr, _c_ptr]
         lib.ta_merge_plan.restype = ctypes.c_int
