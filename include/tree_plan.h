@@ -56,12 +56,14 @@ int tp_grouped_plan(int32_t method, int32_t n, const int32_t *parent, const int3
  * the wave of a 256-row item of a large job that holds the request's rows).
  * Small jobs, in order, go to the candidate item with the fewest attached
  * tiles, then the fewest on the owning wave, then the lowest large job, within
- * xtail_max segments per item and the item's own tile count.
+ * xtail_max segments per item and max(the item's own tile count, min_cap)
+ * attached tiles (min_cap lets the one-tile items of decode-sized layers take
+ * their requests' tails).
  *   large jobs j < n_large: is256[j] (the job's rows use 256-row items),
  *     tiles[j] (LDS tiles its token run streams), requests
  *     req[req_off[j] .. req_off[j+1]) in row order (group query rows each)
  *   small jobs s < n_small: nreq_s[s], first request req0[s], tiles_s[s],
- *     fixed[s] (1: never attached, e.g. a growing decode tail)
+ *     fixed[s] (1: never attached)
  *   requests are ids in [0, nreq); an item covers item_rows rows, a wave
  *     wave_rows of them
  * Outputs: item[s] = index of the item small job s joined (-1: none),
@@ -73,8 +75,8 @@ int tp_grouped_plan(int32_t method, int32_t n, const int32_t *parent, const int3
 int tp_attach_tails(int32_t n_large, const int32_t *is256, const int32_t *tiles, const int32_t *req_off,
                     const int32_t *req, int32_t group, int32_t n_small, const int32_t *nreq_s, const int32_t *req0,
                     const int32_t *tiles_s, const int8_t *fixed, int32_t nreq, int32_t xtail_max,
-                    int32_t wave_rows, int32_t item_rows, int32_t *item, int32_t *lrow, int32_t *item_job,
-                    int32_t *item_row0, int32_t *n_items);
+                    int32_t wave_rows, int32_t item_rows, int32_t min_cap, int32_t *item, int32_t *lrow,
+                    int32_t *item_job, int32_t *item_row0, int32_t *n_items);
 
 /*
  * Device metadata of a prepared plan (the backend's prepare(), cf. the

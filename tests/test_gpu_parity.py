@@ -181,10 +181,20 @@ def test_large_row_tiles_all_kinds(pad, dtype, device):
                             [1] * 20 + [2] * 40 + [3] * 100 + [4] * 140)
     q, k, v = make_inputs(tree, 32, 8, 128, dtype, 9, tcap=tree.storage_tokens + pad)
     ref = oracle_fp32(q, k, v, tree)
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
     for model in (CostModel(max_query_rows=1200, kv_split=512), CostModel(max_query_rows=256, kv_split=190)):
-        say("large-tiles", pad, dtype, model.max_query_rows)
-        out = run(tree, "fixed", model, q, k, v, device, (32, 8, 128))
-        check(out, ref, 0.008, 0.03, "large-tiles")
+        for tile_rows in (256, 128, 64):  # 65..256-row jobs take 256-row items unless tile_rows caps them
+            say("large-tiles", pad, dtype, model.max_query_rows, tile_rows)
+            prepared = prepare(schedule(tree, 32, 8, 128, "fixed", model), qd, tile_rows=tile_rows)
+            n = prepared.abi.n_items
+            allowed = {256: (_native.TA_LARGE64, _native.TA_LARGE256), 128: (_native.TA_LARGE64, _native.TA_LARGE128),
+                       64: (_native.TA_LARGE64,)}[tile_rows]
+            assert all(n[k] == 0 for k in (_native.TA_LARGE64, _native.TA_LARGE128, _native.TA_LARGE256)
+                       if k not in allowed) and n[allowed[-1]] > 0
+            out = attention_matrix(qd, kp, vp, prepared)
+            torch.cuda.synchronize()
+            check(out, ref, 0.008, 0.03, f"large-tiles/{tile_rows}")
 
 
 @pytest.mark.parametrize("name", ["deep", "wide"])
@@ -193,7 +203,8 @@ def test_attention_packs_and_c_abi_phases_agree(name, device):
     tree = shapes.tree(shapes.benchmark_cases()[name])
     q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 3)
     qd, kd, vd = q.to(device), k.to(device), v.to(device)
-    prepared = prepare(schedule(tree, method="cube", model=MI355X_LIKE), qd)
+    # "wide" without attachments: its private tails are TA_TAIL items whose fused kernel merges
+    prepared = prepare(schedule(tree, method="cube", model=MI355X_LIKE), qd, attach_tails=name != "wide")
     a = attention(qd, kd, vd, prepared).clone()
     kp, vp = pack_kv(kd, vd)
     b = attention_matrix(qd, kp, vp, prepared).clone()
@@ -369,6 +380,35 @@ def test_cached_decode_plan_steps(device):
         # zero generated tokens: tails contribute nothing (reference leaves this undefined)
         out = attention_matrix(qd, kp, vp, cached.update(0)).cpu()
         check(out, oracle_fp32(q, k, v, base), 0.008, 0.03, f"decode/{method}/empty-tail")
+
+
+@pytest.mark.parametrize("model_name", ["mi355x", "mi355x-like"])
+def test_attached_growing_tails(model_name, device):
+    """The decode-plan protocol (32 requests, 1024 + 64 prompt, 16 reserved tail tokens each)
+    with the private and growing tails attached to the root's work items: the layer is one
+    segment launch plus the merge, and each step's tail length is read from the attachment
+    records that update() rewrites.  Steps 0, 1, 8 and 16 against the oracle."""
+    base = shapes.tree(shapes.shared_prefix(32, 1024, 64))
+    prefix = base.storage_tokens
+    steps = 16
+    g = torch.Generator().manual_seed(307)
+    q = torch.randn(32, 32, 128, generator=g).bfloat16()
+    k = torch.randn(prefix + 32 * steps, 8, 128, generator=g).bfloat16()
+    v = torch.randn(prefix + 32 * steps, 8, 128, generator=g).bfloat16()
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    model = CostModel.mi355x() if model_name == "mi355x" else MI355X_LIKE
+    cached = CachedDecodePlan(schedule(base, 32, 8, 128, "cube", model), qd, prefix, steps)
+    p = cached.prepared
+    grown = [job for segs in p.attached.values() for job, _ in segs if job.tokens[0] >= prefix]
+    assert len(grown) == 32 and not [j for j in p.jobs if j.tokens[0] >= prefix]
+    assert p.abi.n_items[_native.TA_SMALL] == 0 and p.abi.n_items[_native.TA_TAIL] == 0
+    for step in (0, 1, 8, 16, 3):
+        say("attached growing tails", model_name, step)
+        out = attention_matrix(qd, kp, vp, cached.update(step)).cpu()
+        paths = [p_ + tuple(prefix + r * steps + t for t in range(step)) for r, p_ in enumerate(base.paths)]
+        ref = oracle_fp32(q, k, v, KVTree([], paths))
+        check(out, ref, 0.008, 0.03, f"attached-growing/{model_name}/{step}")
 
 
 def test_reuse_across_calls_and_streams(device):

@@ -3,7 +3,7 @@ import pytest
 import torch
 
 from tree_attention import CostModel, KVTree, schedule, shapes
-from tree_attention import _native
+from tree_attention import _native, kernels
 from tree_attention.kernels import CachedDecodePlan, prepare
 from tree_attention.schedule import Job, Plan
 
@@ -182,16 +182,19 @@ def test_private_tails_attach_to_root_items():
 
 
 def test_attachment_limits():
-    """Tails attach only where the request's rows fit one wave, only up to the item's own
-    tile count, and never for growing decode tails."""
+    """Tails attach only where the request's rows fit one wave, up to XTAIL_MAX segments and
+    the item's own tile count (at least ATTACH_MIN_CAP tiles); growing decode tails attach
+    too, their lengths rewritten in the attachment records by fill_growing."""
     settings = dict(kvheads=1)
     q = torch.empty(80, 4, 32, dtype=torch.float16)   # group 4: 80 requests = 320 rows
     root = Job(tuple(range(80)), tuple(range(0, 64)))  # one tile of root tokens
     tails = [Job((r,), tuple(range(64 + 16 * r, 80 + 16 * r))) for r in range(80)]
     p = prepare(Plan([root] + tails, "x", 0.0, settings), q)
-    # two row tiles (rows 0-255, 256-319) of one job, each may take one tile of tails
-    assert sorted((j, row0, len(s)) for (j, row0), s in p.attached.items()) == [(p.small_jobs, 0, 1),
-                                                                                  (p.small_jobs, 256, 1)]
+    # two row tiles (rows 0-255, 256-319) of one job, one own tile each: each takes
+    # XTAIL_MAX one-tile tails (within the ATTACH_MIN_CAP floor of attached tiles)
+    assert kernels.XTAIL_MAX <= kernels.ATTACH_MIN_CAP
+    assert sorted((j, row0, len(s)) for (j, row0), s in p.attached.items()) == [
+        (p.small_jobs, 0, kernels.XTAIL_MAX), (p.small_jobs, 256, kernels.XTAIL_MAX)]
     assert len(p.jobs) == p.small_jobs + 1
     tree_paths = [tuple(range(0, 64)) + tuple(range(64 + 16 * r, 80 + 16 * r)) for r in range(80)]
     seen = [[] for _ in range(80)]
@@ -202,9 +205,21 @@ def test_attachment_limits():
         for job, _ in segs:
             seen[job.requests[0]].extend(job.tokens)
     assert all(sorted(seen[r]) == list(tree_paths[r]) for r in range(80))
-    # growing tails (fixed_from) stay jobs of their own
-    p = prepare(Plan([root] + tails, "x", 0.0, settings), q, fixed_from=64)
-    assert not p.attached
+    # growing tails (fixed_from) attach the same way; fill_growing sets the klen of those
+    # left as jobs and the token field of every record holding an attached one
+    g = prepare(Plan([root] + tails, "x", 0.0, settings), q, fixed_from=64)
+    assert {k: [(j.requests, lr) for j, lr in v] for k, v in g.attached.items()} == \
+        {k: [(j.requests, lr) for j, lr in v] for k, v in p.attached.items()}
+    njob_tails = sum(job.tokens[0] >= 64 for job in g.jobs)
+    assert njob_tails == 80 - 2 * kernels.XTAIL_MAX
+    assert g.grow_offsets.numel() == njob_tails + 2 * kernels.XTAIL_MAX
+    g.fill_growing(3)
+    assert (g.klen[torch.tensor([j.tokens[0] >= 64 for j in g.jobs])] == 3).all()
+    recs = g.xtail.view(-1, 1 + 3 * kernels.XTAIL_MAX)
+    assert (recs[:, 0] == kernels.XTAIL_MAX).all()
+    assert (recs[:, 2:1 + 3 * kernels.XTAIL_MAX:3] == 3).all()  # every attached segment's token count
+    g.fill_growing(16)
+    assert (recs[:, 2:1 + 3 * kernels.XTAIL_MAX:3] == 16).all() and (g.klen[-1] == 64).all()
     # group 12: request 1's rows 12-23 lie in wave 0; request 2's rows 24-35 straddle waves 0 and 1
     q = torch.empty(24, 12, 32, dtype=torch.float16)
     root = Job(tuple(range(24)), tuple(range(0, 256)))

@@ -383,9 +383,10 @@ extern "C" int tp_grouped_plan(int32_t method, int32_t n, const int32_t *parent,
 extern "C" int tp_attach_tails(int32_t n_large, const int32_t *is256, const int32_t *tiles, const int32_t *req_off,
                                const int32_t *req, int32_t group, int32_t n_small, const int32_t *nreq_s,
                                const int32_t *req0, const int32_t *tiles_s, const int8_t *fixed, int32_t nreq,
-                               int32_t xtail_max, int32_t wave_rows, int32_t item_rows, int32_t *item,
-                               int32_t *lrow, int32_t *item_job, int32_t *item_row0, int32_t *n_items) {
-    if (n_large < 0 || n_small < 0 || nreq <= 0 || group <= 0 || xtail_max < 0 || wave_rows <= 0 ||
+                               int32_t xtail_max, int32_t wave_rows, int32_t item_rows, int32_t min_cap,
+                               int32_t *item, int32_t *lrow, int32_t *item_job, int32_t *item_row0,
+                               int32_t *n_items) {
+    if (n_large < 0 || n_small < 0 || nreq <= 0 || group <= 0 || xtail_max < 0 || wave_rows <= 0 || min_cap < 0 ||
         item_rows <= 0 || item_rows % wave_rows || (n_large && (!is256 || !tiles || !req_off || !req)) ||
         (n_small && (!nreq_s || !req0 || !tiles_s || !fixed || !item || !lrow)) || !item_job || !item_row0 ||
         !n_items)
@@ -428,7 +429,7 @@ extern "C" int tp_attach_tails(int32_t n_large, const int32_t *is256, const int3
         int32_t bt = 0, bw = 0;
         for (const Cand &c : holders[r]) {
             const int32_t t = item_tiles[c.item];
-            if (item_segs[c.item] >= xtail_max || t + n > own[c.item]) continue;
+            if (item_segs[c.item] >= xtail_max || t + n > std::max(own[c.item], min_cap)) continue;
             const int32_t w = wave_tiles[(size_t)c.item * waves + c.wave];
             if (!best || t < bt || (t == bt && (w < bw || (w == bw && c.job < best->job)))) {
                 best = &c;
@@ -499,9 +500,11 @@ extern "C" int tp_build_metadata(int32_t njobs, int32_t small_jobs, const int32_
     int32_t n_rest = 0;
     for (int32_t r = 0; r < nreq; ++r) n_rest += !tail_req[r];
     // row tiles of the large jobs
+    // jobs of 65 .. 256 rows take 256-row items (the pipelined kernel, which
+    // also attends attached segments) unless tile_rows caps the tile lower
     auto kind_of = [&](int64_t rows) {
         if (rows <= 64 || tile_rows <= 64) return 1;
-        if (rows <= 128 || tile_rows <= 128) return 2;
+        if (tile_rows <= 128) return 2;
         return 3;
     };
     static const int tile_of[4] = {0, 64, 128, 256};

@@ -47,7 +47,7 @@ def load(required: bool = True):
             lib.tp_grouped_plan.argtypes = [ctypes.c_int32, ctypes.c_int32] + [_p] * 11
             i32 = ctypes.c_int32
             lib.tp_attach_tails.restype = ctypes.c_int
-            lib.tp_attach_tails.argtypes = ([i32, _p, _p, _p, _p, i32, i32, _p, _p, _p, _p, i32, i32, i32, i32]
+            lib.tp_attach_tails.argtypes = ([i32, _p, _p, _p, _p, i32, i32, _p, _p, _p, _p, i32, i32, i32, i32, i32]
                                             + [_p] * 5)
             lib.tp_build_metadata.restype = ctypes.c_int
             lib.tp_build_metadata.argtypes = [i32, i32, _p, _p, _p, _p, i32, i32, i32, i32, i32, _p, _p, _p, i32,
@@ -98,7 +98,7 @@ def grouped_decisions(tree, method: str, model, qheads: int, kvheads: int, dim: 
 
 
 def attach_tails(large, small, group, is256, large_tiles, small_tiles, fixed, nreq, xtail_max, wave_rows,
-                 item_rows):
+                 item_rows, min_cap):
     """``tp_attach_tails`` over job lists; returns (item per small job or -1, lrow per small job, item keys)."""
     lib = load()
     nl, ns = len(large), len(small)
@@ -121,7 +121,7 @@ def attach_tails(large, small, group, is256, large_tiles, small_tiles, fixed, nr
     ptr = lambda a: _ptr(a if a.size else one)  # noqa: E731
     rc = lib.tp_attach_tails(nl, ptr(is256), ptr(tiles), _ptr(req_off), ptr(req), group, ns, ptr(nreq_s), ptr(req0),
                              ptr(tiles_s), _ptr(fixed if fixed.size else np.zeros(1, np.int8)), nreq, xtail_max,
-                             wave_rows, item_rows, _ptr(item), _ptr(lrow), _ptr(item_job), _ptr(item_row0),
+                             wave_rows, item_rows, min_cap, _ptr(item), _ptr(lrow), _ptr(item_job), _ptr(item_row0),
                              _ptr(n_items))
     if rc != 0:
         raise ValueError(f"tp_attach_tails rejected its arguments (code {rc})")

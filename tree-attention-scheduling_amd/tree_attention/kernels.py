@@ -43,10 +43,15 @@ SMALL_ROWS = 16  # rows of one MFMA block; same threshold as kernels.py:109-110
 
 
 def _large_kind(rows: int, tile_rows: int = 256) -> int:
-    """Row-tile kernel for a job with ``rows`` query rows (tiles of at most ``tile_rows``)."""
+    """Row-tile kernel for a job with ``rows`` query rows (tiles of at most ``tile_rows``).
+
+    Jobs of more than 64 rows take 256-row items (the pipelined kernel, which
+    also attends attached private segments) unless ``tile_rows`` caps the tile
+    at 128 rows.
+    """
     if rows <= 64 or tile_rows <= 64:
         return _native.TA_LARGE64
-    if rows <= 128 or tile_rows <= 128:
+    if tile_rows <= 128:
         return _native.TA_LARGE128
     return _native.TA_LARGE256
 
@@ -80,14 +85,15 @@ class PreparedPlan:
     growing_len: int | None = None  # last CachedDecodePlan.update length of the growing jobs
     qbase_host: list = field(default_factory=list)  # per job: first request if consecutive, else -1
     _unattached: "PreparedPlan | None" = None
+    # positions in ``metadata`` of every growing tail's length: klen of the growing
+    # jobs, the token field of the records of the items the attached ones joined
+    grow_offsets: torch.Tensor | None = None
 
     def fill_growing(self, length: int) -> None:
-        """Set ``klen`` of the growing jobs (tokens from ``fixed_from`` on) to
+        """Set the length of every growing tail (tokens from ``fixed_from`` on) to
         ``length``, here and in the unattached variant (device-side, no sync)."""
-        start = self.options.get("fixed_from")
-        idx = [i for i, job in enumerate(self.jobs) if start is not None and job.tokens[0] >= start]
-        if idx:
-            self.klen.index_fill_(0, torch.tensor(idx, device=self.klen.device), length)
+        if self.grow_offsets is not None:
+            self.metadata.index_fill_(0, self.grow_offsets, length)
         self.growing_len = length
         if self._unattached is not None:
             self._unattached.fill_growing(length)
@@ -143,7 +149,7 @@ def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256, tails=frozense
     big = np.arange(small_jobs, len(jobs))
     rows = np.fromiter((len(jobs[j].requests) * group for j in big), dtype=np.int64, count=big.size)
     kinds = np.where((rows <= 64) | (tile_rows <= 64), _native.TA_LARGE64,
-                     np.where((rows <= 128) | (tile_rows <= 128), _native.TA_LARGE128, _native.TA_LARGE256))
+                     _native.TA_LARGE128 if tile_rows <= 128 else _native.TA_LARGE256)
     for kind, tile in _native.KIND_ROWS.items():
         js = big[kinds == kind]
         ntile = -(-rows[kinds == kind] // tile)
@@ -170,6 +176,9 @@ def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256, tails=frozense
 TOKEN_QUANTUM = 64  # tokens per LDS tile of the segment kernels
 XTAIL_MAX = 4       # private segments one TA_LARGE256 work item takes on (TA_XTAIL_MAX, tree_attn.h)
 WAVE_ROWS = 32      # query rows of one wave of the TA_LARGE256 kernel
+# attached tiles an item may take beyond its own count: the one-tile root items of
+# decode-sized layers take their requests' private and growing tails
+ATTACH_MIN_CAP = 2 * XTAIL_MAX
 
 
 def _tiles(job) -> int:
@@ -192,7 +201,7 @@ def _attach_tails(small, large, group, tile_rows, is_fixed):
     nreq = 1 + max(max(j.requests) for j in (*large, *small))
     item, lrow, keys = _planner.attach_tails(
         large, small, group, is256, [_tiles(j) for j in large], [_tiles(j) for j in small],
-        [bool(is_fixed(j)) for j in small], nreq, XTAIL_MAX, WAVE_ROWS, 256)
+        [bool(is_fixed(j)) for j in small], nreq, XTAIL_MAX, WAVE_ROWS, 256, ATTACH_MIN_CAP)
     attached, left = {}, []
     for job, it, lr in zip(small, item, lrow):
         if it < 0:
@@ -212,9 +221,11 @@ def _attach_tails_py(small, large, group, tile_rows, is_fixed):
     tail's, and the tail needs no launch, work item or partial slot of its own.
     Each tail goes to the candidate item with the fewest attached tiles (then
     the fewest on the owning wave, then the first job), up to ``XTAIL_MAX``
-    segments per item and no more attached tiles than the item's own, so the
-    large kernel's items stay balanced.  Tails for which ``is_fixed`` holds
-    (growing decode tails) are not attached.
+    segments per item and no more attached tiles than the item's own (at least
+    ``ATTACH_MIN_CAP``), so the large kernel's items stay balanced.  Tails for
+    which ``is_fixed`` holds are not attached.  A growing decode tail is
+    balanced by its reserved length; its record reads the current length on
+    the device.
 
     Returns the small jobs left and ``{(large job index, first row): [(job, first job row)]}``.
     """
@@ -251,7 +262,7 @@ def _attach_tails_py(small, large, group, tile_rows, is_fixed):
         best = None
         for J, item, wave, lrow in cands:
             t = item_tiles[item]
-            if item_segs[item] >= XTAIL_MAX or t + n > own[item]:
+            if item_segs[item] >= XTAIL_MAX or t + n > max(own[item], ATTACH_MIN_CAP):
                 continue
             score = (t, wave_tiles[item * waves + wave], J)
             if best is None or score < best[0]:
@@ -489,8 +500,8 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     large = _recut(large, lambda r: -(-len(r) * group // _native.KIND_ROWS[_large_kind(len(r) * group, tile_rows)])
                    * kvheads, n_cu, growing)
     attached = {}
-    if attach_tails:
-        small, attached = _attach_tails(small, large, group, tile_rows, growing)
+    if attach_tails:  # growing tails too: their records' token fields are rewritten by fill_growing
+        small, attached = _attach_tails(small, large, group, tile_rows, lambda job: False)
     # Tails (a request's only small job) stay whole when they alone fill the GPU,
     # so that their work items can merge their requests.
     owners = {}
@@ -540,10 +551,25 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     abi.qbase = qbase_t.data_ptr()
     abi.slot_stride = slot_stride
     keyed = {(j + small_jobs, row0): segs for (j, row0), segs in attached.items()}
+    # Growing decode tails: the length of one lives in klen when it is a job, and in
+    # the token field of the attachment record of every item holding it when it is
+    # attached.  fill_growing writes all of them with one device-side fill.
+    offs = np.cumsum([0] + sizes)
+    grow = [int(offs[3]) + j for j, job in enumerate(jobs) if growing(job)]
+    if attached and fixed_from is not None:
+        slots_of = {key: [k for k, (job, _) in enumerate(segs) if growing(job)] for key, segs in keyed.items()}
+        if any(slots_of.values()):
+            k256 = 10 + _native.TA_LARGE256
+            big = meta["buf"][offs[k256]:offs[k256 + 1]].reshape(-1, 3)
+            for i, (j, row0, _) in enumerate(big.tolist()):
+                for k in slots_of.get((j, row0), ()):
+                    grow.append(int(offs[8]) + i * xstride + 2 + 3 * k)
+    grow_offsets = torch.tensor(grow, dtype=torch.long, device=dev) if grow else None
     return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
                         slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t,
                         keyed, xtail_t if attached else None, plan,
-                        {"tile_rows": tile_rows, "fixed_from": fixed_from}, None, meta["qbase"].tolist())
+                        {"tile_rows": tile_rows, "fixed_from": fixed_from}, None, meta["qbase"].tolist(),
+                        grow_offsets=grow_offsets)
 
 
 def pack_kv(k: torch.Tensor, v: torch.Tensor):
@@ -737,15 +763,14 @@ class CachedDecodePlan:
         self.max_new_tokens = max_new_tokens
         self.prepared = prepare(plan, q, fixed_from=prefix_tokens)
         ordered = self.prepared.jobs
+        # the growing tails that stay jobs (the others are attached to root work items,
+        # their lengths in the attachment records; update() sets both)
         self.tail_indices = torch.tensor([i for i, job in enumerate(ordered) if job.tokens[0] >= prefix_tokens],
-                                         device=q.device)
+                                         device=q.device, dtype=torch.long)
 
     def update(self, generated_tokens):
         """Set every tail's length to ``generated_tokens`` (device-side fill, no sync)."""
         if not 0 <= generated_tokens <= self.max_new_tokens:
             raise ValueError("generated_tokens must be within [0, max_new_tokens]")
-        self.prepared.klen.index_fill_(0, self.tail_indices, generated_tokens)
-        self.prepared.growing_len = generated_tokens
-        if self.prepared._unattached is not None:
-            self.prepared._unattached.fill_growing(generated_tokens)
+        self.prepared.fill_growing(generated_tokens)
         return self.prepared

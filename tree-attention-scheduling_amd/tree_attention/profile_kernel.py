@@ -21,9 +21,10 @@ import statistics
 
 import torch
 
-from . import CostModel, schedule, shapes
+from . import CostModel, KVTree, schedule, shapes
 from . import _native
-from .kernels import attention_matrix, launch_durations_us, merge, pack_kv, prepare, segment, tail_merge
+from .kernels import (CachedDecodePlan, attention_matrix, launch_durations_us, merge, pack_kv, prepare, segment,
+                      tail_merge)
 
 KINDS = {"small": _native.TA_SMALL, "large64": _native.TA_LARGE64, "large128": _native.TA_LARGE128,
          "large256": _native.TA_LARGE256, "tail": _native.TA_TAIL}
@@ -31,7 +32,8 @@ KINDS = {"small": _native.TA_SMALL, "large64": _native.TA_LARGE64, "large128": _
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--shape", default="wide_long")
+    ap.add_argument("--shape", default="wide_long",
+                    help="a scripts/benchmark.py case, or qwen3_4b (the Qwen3-4B-shaped decode workload's tree)")
     ap.add_argument("--shared-prefix", default=None, metavar="R,ROOT,PRIVATE",
                     help="instead of --shape: R requests on one ROOT-token root with PRIVATE-token tails")
     ap.add_argument("--method", default="cube")
@@ -42,6 +44,10 @@ def main(argv=None):
     ap.add_argument("--pools", type=int, default=8)
     ap.add_argument("--heads", default="32,8,128")
     ap.add_argument("--tile-rows", type=int, default=256)
+    ap.add_argument("--decode", type=int, default=0, metavar="N",
+                    help="decode layer: a CachedDecodePlan over the shape's plan with N reserved tail tokens "
+                         "per request (scripts/benchmark_decode_plan.py's protocol), updated to --step")
+    ap.add_argument("--step", type=int, default=1, help="generated tokens of each tail with --decode")
     ap.add_argument("--stamp", action="store_true",
                     help="also report the median kernel duration from dispatch stamps (library kernels only)")
     ap.add_argument("--param", action="append", default=[],
@@ -52,9 +58,11 @@ def main(argv=None):
         r, root, private = map(int, args.shared_prefix.split(","))
         spec = shapes.shared_prefix(r, root, private)
         args.shape = f"shared_prefix({r},{root},{private})"
+    elif args.shape == "qwen3_4b":  # the Qwen3-4B-shaped decode workload's prompt tree (token sequences)
+        spec = None
     else:
         spec = shapes.benchmark_cases()[args.shape]
-    tree = shapes.tree(spec)
+    tree = KVTree.from_sequences(shapes.qwen3_4b_workload()) if spec is None else shapes.tree(spec)
     model = CostModel.mi355x() if args.cost_model == "mi355x" else CostModel()
     for kv in args.param:
         key, val = kv.split("=")
@@ -62,11 +70,19 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(101)
     q = torch.randn(len(tree.paths), hq, d, generator=g).bfloat16().to(dev)
-    k = torch.randn(tree.storage_tokens, hk, d, generator=g).bfloat16().to(dev)
-    v = torch.randn(tree.storage_tokens, hk, d, generator=g).bfloat16().to(dev)
+    tokens = tree.storage_tokens + len(tree.paths) * args.decode
+    tokens = -(-tokens // 8) * 8  # pool capacity a multiple of 8, as the model adapter allocates it
+    k = torch.randn(tokens, hk, d, generator=g).bfloat16().to(dev)
+    v = torch.randn(tokens, hk, d, generator=g).bfloat16().to(dev)
     kp, vp = pack_kv(k, v)
     pools = [(kp, vp)] + [(kp.clone(), vp.clone()) for _ in range(args.pools - 1)]
-    prepared = prepare(schedule(tree, hq, hk, d, args.method, model), q, args.tile_rows)
+    plan = schedule(tree, hq, hk, d, args.method, model)
+    if args.decode:
+        cached = CachedDecodePlan(plan, q, tree.storage_tokens, args.decode)
+        prepared = cached.update(args.step)
+        args.shape += f" + {args.decode}-token decode tails at step {args.step}"
+    else:
+        prepared = prepare(plan, q, args.tile_rows)
     attention_matrix(q, kp, vp, prepared)  # partials exist before a lone merge
 
     if args.kernel == "copy":
