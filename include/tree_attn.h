@@ -55,9 +55,9 @@ extern "C" {
                            is the last of its request's slots. */
 #define TA_NKINDS 5
 
-/* attached private segments per TA_LARGE256 work item (ta_plan.xtail) */
+/* attached segments per TA_LARGE256 work item (ta_plan.xtail) */
 #define TA_XTAIL_MAX 4
-#define TA_XTAIL_STRIDE (1 + 3 * TA_XTAIL_MAX)
+#define TA_XTAIL_STRIDE (1 + 4 * TA_XTAIL_MAX)
 
 #define TA_ERR_ARG 1001      /* null pointer, bad size or unsupported shape */
 #define TA_ERR_ALIGN 1002    /* q / kp / vp / part / out not 16-byte aligned, lse not 8-byte */
@@ -90,14 +90,15 @@ typedef struct ta_plan {
     int32_t njobs, maxr, maxs, nreq, nslot;
     int32_t hq, hk, d, dtype;
     int32_t n_rest;
-    /* Attached private segments of the TA_LARGE256 items (NULL: none), an
-     * execution detail with no counterpart in the reference: xtail_stride
+    /* Attached segments of the TA_LARGE256 items (NULL: none), an execution
+     * detail with no counterpart in the reference: xtail_stride
      * (= TA_XTAIL_STRIDE) ints per TA_LARGE256 item -- the number of segments
-     * n <= TA_XTAIL_MAX, then (first physical token, tokens, first job row)
-     * for each of the n.  The segment's tokens
-     * belong to the request whose group query rows start at that job row
-     * (rows of one wave, 32 rows); the item folds them into that request's
-     * partial rows, so the segment has no partial slot of its own.  Needs
+     * n <= TA_XTAIL_MAX, then (first physical token, tokens, first job row,
+     * rows) for each of the n.  A segment's tokens belong to the query rows
+     * [first job row, first job row + rows) of the item's job, which lie in
+     * one wave (32 rows): a private tail (the group rows of one request) or a
+     * node of a few consecutive requests.  The item folds the tokens into those
+     * rows' partials, so the segment has no partial slot of its own.  Needs
      * tcap % 8 == 0 (ta_attention_matrix returns TA_ERR_ARG otherwise). */
     const int32_t *xtail;
     int32_t xtail_stride;

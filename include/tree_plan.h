@@ -50,11 +50,12 @@ int tp_grouped_plan(int32_t method, int32_t n, const int32_t *parent, const int3
                     const int64_t *iparams, int8_t *pushed, double *total);
 
 /*
- * Attachment of private tails to 256-row work items, a step of the backend's
+ * Attachment of small segments to 256-row work items, a step of the backend's
  * prepare() with no counterpart in the reference (its jobs each get their own
- * launch work; here a request's single-request job may instead be attended by
- * the wave of a 256-row item of a large job that holds the request's rows).
- * Small jobs, in order, go to the candidate item with the fewest attached
+ * launch work; here a job whose rows fit one wave -- a private tail, or a
+ * node of a few requests -- may instead be attended by the wave of a 256-row
+ * item of a large job that holds all of its requests at consecutive rows).
+ * Candidate jobs, in order, go to the candidate item with the fewest attached
  * tiles, then the fewest on the owning wave, then the lowest large job, within
  * xtail_max segments per item and max(the item's own tile count, min_cap)
  * attached tiles (min_cap lets the one-tile items of decode-sized layers take
@@ -62,18 +63,18 @@ int tp_grouped_plan(int32_t method, int32_t n, const int32_t *parent, const int3
  *   large jobs j < n_large: is256[j] (the job's rows use 256-row items),
  *     tiles[j] (LDS tiles its token run streams), requests
  *     req[req_off[j] .. req_off[j+1]) in row order (group query rows each)
- *   small jobs s < n_small: nreq_s[s], first request req0[s], tiles_s[s],
- *     fixed[s] (1: never attached)
+ *   candidate jobs s < n_small: requests sreq[sreq_off[s] .. sreq_off[s+1])
+ *     in row order, tiles_s[s], fixed[s] (1: never attached)
  *   requests are ids in [0, nreq); an item covers item_rows rows, a wave
  *     wave_rows of them
- * Outputs: item[s] = index of the item small job s joined (-1: none),
- * lrow[s] = its request's first row in the large job; the item list
+ * Outputs: item[s] = index of the item candidate s joined (-1: none),
+ * lrow[s] = the first row of its requests in the large job; the item list
  * (item_job[i], item_row0[i]) for i < n_items[0], in large-job order (the
  * caller sizes it: the sum over 256-row jobs of ceil(rows / item_rows)).
  * Returns 0, or 1 for invalid arguments.
  */
 int tp_attach_tails(int32_t n_large, const int32_t *is256, const int32_t *tiles, const int32_t *req_off,
-                    const int32_t *req, int32_t group, int32_t n_small, const int32_t *nreq_s, const int32_t *req0,
+                    const int32_t *req, int32_t group, int32_t n_small, const int32_t *sreq_off, const int32_t *sreq,
                     const int32_t *tiles_s, const int8_t *fixed, int32_t nreq, int32_t xtail_max,
                     int32_t wave_rows, int32_t item_rows, int32_t min_cap, int32_t *item, int32_t *lrow,
                     int32_t *item_job, int32_t *item_row0, int32_t *n_items);

@@ -70,7 +70,8 @@ def test_xtail_record_layout_matches_header():
     from tree_attention import kernels
     header = (Path(__file__).resolve().parents[1] / "include" / "tree_attn.h").read_text()
     assert int(re.search(r"#define TA_XTAIL_MAX (\d+)", header).group(1)) == kernels.XTAIL_MAX
-    assert "#define TA_XTAIL_STRIDE (1 + 3 * TA_XTAIL_MAX)" in header
+    assert "#define TA_XTAIL_STRIDE (1 + 4 * TA_XTAIL_MAX)" in header
+    assert kernels.XTAIL_FIELDS == 4
 
 
 def test_decode_append_rejects_host_slots_outside_the_pool():

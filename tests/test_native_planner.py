@@ -136,7 +136,9 @@ def test_uncovered_cases_fall_back_or_raise():
 
 @pytest.mark.parametrize("seed", range(8))
 def test_native_tail_attachment_equals_python(seed):
-    """tp_attach_tails against kernels._attach_tails_py on random job sets: same attachments, same order."""
+    """tp_attach_tails against kernels._attach_tails_py on random job sets: same attachments, same
+    order, for single-request tails and for candidates of a few requests, scattered or consecutive
+    (attachable only at consecutive rows of one wave)."""
     from tree_attention import kernels
     from tree_attention.schedule import Job
     rng = random.Random(seed)
@@ -149,7 +151,14 @@ def test_native_tail_attachment_equals_python(seed):
         base += n
     small = []
     for _ in range(rng.randint(0, 200)):
-        reqs = (rng.randrange(nreq),) if rng.random() < 0.85 else tuple(sorted(rng.sample(range(nreq), 2)))
+        u = rng.random()
+        if u < 0.7:
+            reqs = (rng.randrange(nreq),)
+        elif u < 0.85:
+            reqs = tuple(sorted(rng.sample(range(nreq), 2)))
+        else:  # a node over consecutive requests
+            r0 = rng.randrange(nreq)
+            reqs = tuple(range(r0, min(nreq, r0 + rng.randint(2, 8))))
         n = rng.randint(1, 300)
         small.append(Job(reqs, tuple(range(base, base + n))))
         base += n

@@ -3,7 +3,7 @@ import pytest
 import torch
 
 from tree_attention import CostModel, KVTree, schedule, shapes
-from tree_attention import _native, kernels
+from tree_attention import _native, _planner, kernels
 from tree_attention.kernels import CachedDecodePlan, prepare
 from tree_attention.schedule import Job, Plan
 
@@ -174,7 +174,8 @@ def test_private_tails_attach_to_root_items():
     for rec, (j, row0, h) in zip(xt, items):
         segs = p.attached[(j, row0)]
         assert rec[0] == len(segs)
-        assert rec[1:1 + 3 * len(segs)] == [v for tail, lrow in segs for v in (tail.tokens[0], len(tail.tokens), lrow)]
+        assert rec[1:1 + 4 * len(segs)] == [v for tail, lrow in segs
+                                            for v in (tail.tokens[0], len(tail.tokens), lrow, 4)]
     # without attachment the tails are TA_TAIL jobs again
     p2 = prepare(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q, attach_tails=False)
     assert not p2.attached and p2.xtail is None and p2.abi.xtail is None
@@ -215,11 +216,12 @@ def test_attachment_limits():
     assert g.grow_offsets.numel() == njob_tails + 2 * kernels.XTAIL_MAX
     g.fill_growing(3)
     assert (g.klen[torch.tensor([j.tokens[0] >= 64 for j in g.jobs])] == 3).all()
-    recs = g.xtail.view(-1, 1 + 3 * kernels.XTAIL_MAX)
+    recs = g.xtail.view(-1, 1 + 4 * kernels.XTAIL_MAX)
     assert (recs[:, 0] == kernels.XTAIL_MAX).all()
-    assert (recs[:, 2:1 + 3 * kernels.XTAIL_MAX:3] == 3).all()  # every attached segment's token count
+    assert (recs[:, 2:1 + 4 * kernels.XTAIL_MAX:4] == 3).all()  # every attached segment's token count
+    assert (recs[:, 4:1 + 4 * kernels.XTAIL_MAX:4] == 4).all()  # and its rows (one request, group 4)
     g.fill_growing(16)
-    assert (recs[:, 2:1 + 3 * kernels.XTAIL_MAX:3] == 16).all() and (g.klen[-1] == 64).all()
+    assert (recs[:, 2:1 + 4 * kernels.XTAIL_MAX:4] == 16).all() and (g.klen[-1] == 64).all()
     # group 12: request 1's rows 12-23 lie in wave 0; request 2's rows 24-35 straddle waves 0 and 1
     q = torch.empty(24, 12, 32, dtype=torch.float16)
     root = Job(tuple(range(24)), tuple(range(0, 256)))
@@ -245,3 +247,62 @@ def test_affine_slot_layout():
         tree = shapes.tree(spec)
         q = torch.empty(len(tree.paths), 32, 128, dtype=torch.bfloat16)
         assert prepare(schedule(tree, method="cube", model=CostModel.mi355x()), q).abi.slot_stride == 0
+
+
+def test_nodes_of_a_wave_attach():
+    """A job of a few requests whose rows lie in one wave of a 256-row item (a branch node over
+    consecutive requests) attaches like a private tail; its record carries its row count, and
+    the layer keeps one segment launch.  Jobs whose requests are not consecutive rows of one
+    wave in the large job stay jobs."""
+    settings = dict(kvheads=1)
+    q = torch.empty(32, 4, 32, dtype=torch.float16)  # 32 requests x group 4 = 128 rows, waves of 8 requests
+    root = Job(tuple(range(32)), tuple(range(0, 512)))
+    branches = [Job(tuple(range(8 * b, 8 * b + 8)), tuple(range(512 + 64 * b, 576 + 64 * b))) for b in range(4)]
+    misaligned = Job(tuple(range(4, 12)), tuple(range(800, 864)))    # rows 16-47: two waves
+    gapped = Job((1, 3), tuple(range(900, 932)))                       # rows 4-7 and 12-15: not consecutive
+    # root: 8 one-tile items of 4 segments each; 16 tails leave room for the nodes
+    tails = [Job((r,), tuple(range(1000 + 16 * r, 1016 + 16 * r))) for r in range(0, 32, 2)]
+    plan = Plan([root] + branches + [misaligned, gapped] + tails, "x", 0.0, settings)
+    for native in (True, False):
+        if native and not _planner.available():
+            continue
+        p = prepare(plan, q) if native else _prepare_python_attach(plan, q)
+        segs = [(job.requests, lrow) for s in p.attached.values() for job, lrow in s]
+        for b in range(4):
+            assert (tuple(range(8 * b, 8 * b + 8)), 32 * b) in segs
+        assert not any(req == misaligned.requests or req == gapped.requests for req, _ in segs)
+        left = [job.requests for job in p.jobs]
+        assert misaligned.requests in left and gapped.requests in left
+        assert all(job.requests not in [br.requests for br in branches] for job in p.jobs)
+        for (j, row0), s in p.attached.items():
+            rec = p.xtail.view(-1, p.abi.xtail_stride)[[i for i, (jj, r0, h) in enumerate(
+                p.items[_native.TA_LARGE256].view(-1, 3).tolist()) if (jj, r0) == (j, row0)][0]].tolist()
+            assert rec[4:1 + 4 * len(s):4] == [4 * len(job.requests) for job, _ in s]
+        assert _covers_paths_plan(p, plan, 32)
+
+
+def _prepare_python_attach(plan, q):
+    """prepare() with the Python attachment (kernels._attach_tails_py) instead of the host library's."""
+    orig = kernels._attach_tails
+    kernels._attach_tails = kernels._attach_tails_py
+    try:
+        return prepare(plan, q)
+    finally:
+        kernels._attach_tails = orig
+
+
+def _covers_paths_plan(p, plan, nreq):
+    """Every request's tokens in the prepared jobs and attachments are exactly its plan tokens."""
+    want = [[] for _ in range(nreq)]
+    for job in plan.jobs:
+        for r in job.requests:
+            want[r].extend(job.tokens)
+    seen = [[] for _ in range(nreq)]
+    for job in p.jobs:
+        for r in job.requests:
+            seen[r].extend(job.tokens)
+    for segs in p.attached.values():
+        for job, _ in segs:
+            for r in job.requests:
+                seen[r].extend(job.tokens)
+    return all(sorted(seen[r]) == sorted(want[r]) for r in range(nreq))

@@ -369,26 +369,26 @@ extern "C" int tp_grouped_plan(int32_t method, int32_t n, const int32_t *parent,
     return 0;
 }
 
-// Attachment of private tails to 256-row work items (tree_attention/kernels.py
-// _attach_tails): small jobs of one request go, in order, to the candidate
-// item (a 256-row item of a large job whose rows include the request's, all
-// in one wave) with the fewest attached tiles, then the fewest on the owning
-// wave, then the lowest large job, within `xtail_max` segments and the item's
-// own tile count.
+// Attachment of small segments to 256-row work items (tree_attention/kernels.py
+// _attach_tails): candidate jobs go, in order, to the candidate item (a 256-row
+// item of a large job whose requests include the candidate's, at consecutive
+// rows that lie in one wave) with the fewest attached tiles, then the fewest on
+// the owning wave, then the lowest large job, within `xtail_max` segments and
+// the item's own tile count.
 //   large jobs J < n_large: is256[J], tiles[J], requests req[req_off[J] .. req_off[J+1])
-//   small jobs s < n_small: nreq_s[s], first request req0[s], tiles_s[s], fixed[s]
+//   candidate jobs s < n_small: requests sreq[sreq_off[s] .. sreq_off[s+1]), tiles_s[s], fixed[s]
 // Writes item[s] (index into the item list, -1: not attached) and lrow[s]
-// (first job row of the request), the item list (item_job, item_row0) and
-// n_items[0].  Returns 0, or 1 for invalid arguments.
+// (first job row of the candidate's requests), the item list (item_job,
+// item_row0) and n_items[0].  Returns 0, or 1 for invalid arguments.
 extern "C" int tp_attach_tails(int32_t n_large, const int32_t *is256, const int32_t *tiles, const int32_t *req_off,
-                               const int32_t *req, int32_t group, int32_t n_small, const int32_t *nreq_s,
-                               const int32_t *req0, const int32_t *tiles_s, const int8_t *fixed, int32_t nreq,
+                               const int32_t *req, int32_t group, int32_t n_small, const int32_t *sreq_off,
+                               const int32_t *sreq, const int32_t *tiles_s, const int8_t *fixed, int32_t nreq,
                                int32_t xtail_max, int32_t wave_rows, int32_t item_rows, int32_t min_cap,
                                int32_t *item, int32_t *lrow, int32_t *item_job, int32_t *item_row0,
                                int32_t *n_items) {
     if (n_large < 0 || n_small < 0 || nreq <= 0 || group <= 0 || xtail_max < 0 || wave_rows <= 0 || min_cap < 0 ||
         item_rows <= 0 || item_rows % wave_rows || (n_large && (!is256 || !tiles || !req_off || !req)) ||
-        (n_small && (!nreq_s || !req0 || !tiles_s || !fixed || !item || !lrow)) || !item_job || !item_row0 ||
+        (n_small && (!sreq_off || !sreq || !tiles_s || !fixed || !item || !lrow)) || !item_job || !item_row0 ||
         !n_items)
         return 1;
     struct Cand {
@@ -422,12 +422,22 @@ extern "C" int tp_attach_tails(int32_t n_large, const int32_t *is256, const int3
     for (int32_t s = 0; s < n_small; ++s) {
         item[s] = -1;
         lrow[s] = 0;
-        const int32_t r = req0[s];
-        if (nreq_s[s] != 1 || fixed[s] || r < 0 || r >= nreq) continue;
+        const int32_t nr = sreq_off[s + 1] - sreq_off[s];
+        if (nr <= 0 || fixed[s]) continue;
+        const int32_t *sr = sreq + sreq_off[s];
+        const int32_t r = sr[0];
+        if (r < 0 || r >= nreq) continue;
         const int32_t n = tiles_s[s];
         const Cand *best = nullptr;
         int32_t bt = 0, bw = 0;
         for (const Cand &c : holders[r]) {
+            // every request of the candidate at the next rows of the same wave
+            if (c.lrow % wave_rows + (int64_t)nr * group > wave_rows) continue;
+            const int32_t pos = req_off[c.job] + c.lrow / group;
+            if (pos + nr > req_off[c.job + 1]) continue;
+            bool same = true;
+            for (int32_t i = 1; i < nr && same; ++i) same = req[pos + i] == sr[i];
+            if (!same) continue;
             const int32_t t = item_tiles[c.item];
             if (item_segs[c.item] >= xtail_max || t + n > std::max(own[c.item], min_cap)) continue;
             const int32_t w = wave_tiles[(size_t)c.item * waves + c.wave];

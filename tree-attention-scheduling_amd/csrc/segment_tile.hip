@@ -626,30 +626,31 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     auto tile_stage = [&](int t) { return lds + (t % STAGES) * T::ELEMS; };
     auto stage = [&](int g) { return tile_stage(g >> 1); };  // stage of step g's tile
 
-    // Attached private segments (xtail record of this item: count, then
-    // (first token, tokens, first job row) for up to TA_XTAIL_MAX segments)
+    // Attached segments (xtail record of this item: count, then (first token,
+    // tokens, first job row, rows) for up to TA_XTAIL_MAX segments)
     // follow the job's own tiles in one tile sequence through the same LDS
     // stages.  The record is read at once (constant address space: one batch
     // of scalar loads, no chain of dependent loads) into per-segment values
     // that unrolled loops index with constants.
     constexpr int XM = TA_XTAIL_MAX;
-    int rec[1 + 3 * XM];
+    constexpr int XF = 4;  // fields per segment
+    int rec[1 + XF * XM];
     if (p.xtail) {
         const __attribute__((address_space(4))) int32_t *xt =
             (const __attribute__((address_space(4))) int32_t *)(p.xtail + (size_t)item * p.xtail_stride);
 #pragma unroll
-        for (int i = 0; i < 1 + 3 * XM; ++i) rec[i] = xt[i];
+        for (int i = 0; i < 1 + XF * XM; ++i) rec[i] = xt[i];
     } else {
 #pragma unroll
-        for (int i = 0; i < 1 + 3 * XM; ++i) rec[i] = 0;
+        for (int i = 0; i < 1 + XF * XM; ++i) rec[i] = 0;
     }
     const int nx = min(max(rec[0], 0), XM);
     int xs[XM], xe[XM], xfirst[XM], xn[XM];  // clamped token range, first tile and tiles of each segment
     int ntot = ntiles;
 #pragma unroll
     for (int k = 0; k < XM; ++k) {
-        xs[k] = max(0, rec[1 + 3 * k]);
-        xe[k] = xs[k] + max(0, min(rec[2 + 3 * k], p.tcap - xs[k]));
+        xs[k] = max(0, rec[1 + XF * k]);
+        xe[k] = xs[k] + max(0, min(rec[2 + XF * k], p.tcap - xs[k]));
         xn[k] = k < nx && xe[k] > xs[k] ? (xe[k] - (xs[k] & ~7) + T::TT - 1) / T::TT : 0;
         xfirst[k] = ntot;
         ntot += xn[k];
@@ -777,12 +778,12 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
             __builtin_amdgcn_s_barrier();  // the round's tiles landed
 #pragma unroll
             for (int k = 0; k < XM; ++k) {
-                const int rlo = rec[3 + 3 * k] - wrow0;  // segment rows in this wave: [rlo, rlo + group)
+                const int rlo = rec[3 + XF * k] - wrow0;  // segment rows in this wave: [rlo, rlo + rows)
                 if (xn[k] > 0 && active && rlo >= 0 && rlo < 16 * NB) {
                     for (int i = max(0, r0 - xfirst[k]); i < xn[k] && xfirst[k] + i < r1; ++i) {
                         const int t0 = (xs[k] & ~7) + i * T::TT;
                         acc.tail_tile(tile_stage(xfirst[k] + i), qf, of, max(0, xs[k] - t0), min(T::TT, xe[k] - t0),
-                                      rlo, rlo + p.group, row, g4, c, rc);
+                                      rlo, rlo + rec[4 + XF * k], row, g4, c, rc);
                     }
                 }
             }

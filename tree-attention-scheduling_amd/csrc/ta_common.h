@@ -143,8 +143,8 @@ struct SegParams {
     u16 *out;
     int maxs;
     // TA_LARGE256 items only (nullable): per item xtail_stride (=
-    // TA_XTAIL_STRIDE) ints -- the number of attached private segments (at
-    // most TA_XTAIL_MAX), then (first token, tokens, first job row) of each;
+    // TA_XTAIL_STRIDE) ints -- the number of attached segments (at most
+    // TA_XTAIL_MAX), then (first token, tokens, first job row, rows) of each;
     // the item folds them into its rows' partials
     const int32_t *xtail;
     int xtail_stride;

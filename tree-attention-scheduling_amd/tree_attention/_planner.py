@@ -99,7 +99,7 @@ def grouped_decisions(tree, method: str, model, qheads: int, kvheads: int, dim: 
 
 def attach_tails(large, small, group, is256, large_tiles, small_tiles, fixed, nreq, xtail_max, wave_rows,
                  item_rows, min_cap):
-    """``tp_attach_tails`` over job lists; returns (item per small job or -1, lrow per small job, item keys)."""
+    """``tp_attach_tails`` over job lists; returns (item per candidate job or -1, its first row, item keys)."""
     lib = load()
     nl, ns = len(large), len(small)
     req_off = np.zeros(nl + 1, dtype=np.int32)
@@ -107,8 +107,9 @@ def attach_tails(large, small, group, is256, large_tiles, small_tiles, fixed, nr
     req = np.fromiter(chain.from_iterable(j.requests for j in large), dtype=np.int32, count=int(req_off[-1]))
     is256 = np.asarray(is256, dtype=np.int32)
     tiles = np.asarray(large_tiles, dtype=np.int32)
-    nreq_s = np.fromiter((len(j.requests) for j in small), dtype=np.int32, count=ns)
-    req0 = np.fromiter((j.requests[0] for j in small), dtype=np.int32, count=ns)
+    sreq_off = np.zeros(ns + 1, dtype=np.int32)
+    np.cumsum([len(j.requests) for j in small], out=sreq_off[1:])
+    sreq = np.fromiter(chain.from_iterable(j.requests for j in small), dtype=np.int32, count=int(sreq_off[-1]))
     tiles_s = np.asarray(small_tiles, dtype=np.int32)
     fixed = np.asarray(fixed, dtype=np.int8)
     cap = int(sum(-(-len(j.requests) * group // item_rows) for j, b in zip(large, is256) if b))
@@ -119,7 +120,7 @@ def attach_tails(large, small, group, is256, large_tiles, small_tiles, fixed, nr
     n_items = np.zeros(1, dtype=np.int32)
     one = np.zeros(1, dtype=np.int32)
     ptr = lambda a: _ptr(a if a.size else one)  # noqa: E731
-    rc = lib.tp_attach_tails(nl, ptr(is256), ptr(tiles), _ptr(req_off), ptr(req), group, ns, ptr(nreq_s), ptr(req0),
+    rc = lib.tp_attach_tails(nl, ptr(is256), ptr(tiles), _ptr(req_off), ptr(req), group, ns, _ptr(sreq_off), ptr(sreq),
                              ptr(tiles_s), _ptr(fixed if fixed.size else np.zeros(1, np.int8)), nreq, xtail_max,
                              wave_rows, item_rows, min_cap, _ptr(item), _ptr(lrow), _ptr(item_job), _ptr(item_row0),
                              _ptr(n_items))

@@ -174,7 +174,8 @@ def _build_items(jobs, small_jobs, group, kvheads, tile_rows=256, tails=frozense
 
 
 TOKEN_QUANTUM = 64  # tokens per LDS tile of the segment kernels
-XTAIL_MAX = 4       # private segments one TA_LARGE256 work item takes on (TA_XTAIL_MAX, tree_attn.h)
+XTAIL_MAX = 4       # segments one TA_LARGE256 work item takes on (TA_XTAIL_MAX, tree_attn.h)
+XTAIL_FIELDS = 4    # per segment: first token, tokens, first job row, rows (TA_XTAIL_STRIDE, tree_attn.h)
 WAVE_ROWS = 32      # query rows of one wave of the TA_LARGE256 kernel
 # attached tiles an item may take beyond its own count: the one-tile root items of
 # decode-sized layers take their requests' private and growing tails
@@ -189,6 +190,7 @@ def _tiles(job) -> int:
 
 def _attach_tails(small, large, group, tile_rows, is_fixed):
     """``_attach_tails_py`` through the host library (``tp_attach_tails``) when it is built.
+    ``small`` are the candidate jobs (any job whose rows fit one wave).
 
     Both give the same attachments in the same order.
     """
@@ -212,22 +214,24 @@ def _attach_tails(small, large, group, tile_rows, is_fixed):
 
 
 def _attach_tails_py(small, large, group, tile_rows, is_fixed):
-    """Fold single-request small jobs into TA_LARGE256 work items of large jobs.
+    """Fold jobs whose rows fit one wave into TA_LARGE256 work items of large jobs.
 
-    A small job of one request ``r`` (a private tail) can be attended by any
-    256-row work item of a large job whose rows include ``r``'s: the wave that
-    holds those rows attends the tail's tokens into the same online-softmax
-    state, so the item's partial for ``r`` covers the job's tokens and the
-    tail's, and the tail needs no launch, work item or partial slot of its own.
-    Each tail goes to the candidate item with the fewest attached tiles (then
-    the fewest on the owning wave, then the first job), up to ``XTAIL_MAX``
+    A candidate job over requests ``r0 .. rn-1`` (a private tail, or a node of
+    a few requests) can be attended by any 256-row work item of a large job
+    that holds those requests at consecutive rows within one wave: that wave
+    attends the job's tokens into the same online-softmax state, so the item's
+    partials for ``r0 .. rn-1`` cover the large job's tokens and the job's, and
+    the job needs no launch, work item or partial slot of its own.  Each job
+    goes to the candidate item with the fewest attached tiles (then the fewest
+    on the owning wave, then the first large job), up to ``XTAIL_MAX``
     segments per item and no more attached tiles than the item's own (at least
-    ``ATTACH_MIN_CAP``), so the large kernel's items stay balanced.  Tails for
+    ``ATTACH_MIN_CAP``), so the large kernel's items stay balanced.  Jobs for
     which ``is_fixed`` holds are not attached.  A growing decode tail is
     balanced by its reserved length; its record reads the current length on
     the device.
 
-    Returns the small jobs left and ``{(large job index, first row): [(job, first job row)]}``.
+    Returns the candidate jobs left and
+    ``{(large job index, first row): [(job, first job row)]}``.
     """
     # the 256-row work items: their key (large job index, first row) and the
     # tiles their own job streams; holders[r]: (job, item, wave, first job row)
@@ -246,6 +250,12 @@ def _attach_tails_py(small, large, group, tile_rows, is_fixed):
             lrow = pos * group
             if lrow % WAVE_ROWS + group <= WAVE_ROWS:
                 holders.setdefault(r, []).append((J, first + lrow // 256, lrow % 256 // WAVE_ROWS, lrow))
+
+    def fits(J, lrow, reqs):  # reqs at consecutive rows of one wave of large[J], from lrow on
+        held = large[J].requests
+        pos = lrow // group
+        return (lrow % WAVE_ROWS + len(reqs) * group <= WAVE_ROWS
+                and tuple(held[pos:pos + len(reqs)]) == tuple(reqs))
     if not holders:
         return small, {}
     waves = 256 // WAVE_ROWS
@@ -253,14 +263,15 @@ def _attach_tails_py(small, large, group, tile_rows, is_fixed):
     attached = {}
     left = []
     for job in small:
-        r = job.requests[0]
-        cands = holders.get(r) if len(job.requests) == 1 else None
+        cands = holders.get(job.requests[0])
         if not cands or is_fixed(job):
             left.append(job)
             continue
         n = _tiles(job)
         best = None
         for J, item, wave, lrow in cands:
+            if len(job.requests) > 1 and not fits(J, lrow, job.requests):
+                continue
             t = item_tiles[item]
             if item_segs[item] >= XTAIL_MAX or t + n > max(own[item], ATTACH_MIN_CAP):
                 continue
@@ -347,6 +358,13 @@ def _request_error(jobs, nreq):
     return ValueError("a request is outside q's requests")
 
 
+def _xtail_record(segs, group):
+    """The attachment record of one TA_LARGE256 item: the segment count, then
+    (first token, tokens, first job row, rows) of each segment."""
+    return [len(segs)] + [x for job, lrow in segs for x in (job.tokens[0], len(job.tokens), lrow,
+                                                             len(job.requests) * group)]
+
+
 def _metadata_sections(njobs, maxr, nreq, maxs, n_rest, n_l256, attached, xstride, n_items):
     """Shapes of the int32 metadata sections, in upload order (tp_build_metadata's order)."""
     return ([(njobs, maxr), (njobs, 1), (njobs,), (njobs,), (nreq, maxs), (nreq,), (njobs,), (n_rest,),
@@ -364,8 +382,7 @@ def _metadata_native(jobs, small_jobs, nreq, group, kvheads, tile_rows, attached
     att_row0 = np.fromiter((r0 for _, r0 in attached), dtype=np.int32, count=len(attached))
     att_rec = np.zeros((len(attached), xstride), dtype=np.int32)
     for i, segs in enumerate(attached.values()):
-        rec = [len(segs)] + [x for job, lrow in segs for x in (job.tokens[0], len(job.tokens), lrow)]
-        att_rec[i, :len(rec)] = rec
+        att_rec[i, :1 + XTAIL_FIELDS * len(segs)] = _xtail_record(segs, group)
     try:
         sizes, buf = _planner.build_metadata(qlen, req, kstart, klen, small_jobs, nreq, group, kvheads, tile_rows,
                                              att_job, att_row0, att_rec, xstride)
@@ -424,14 +441,13 @@ def _metadata_numpy(jobs, small_jobs, nreq, group, kvheads, tile_rows, attached,
         affine = np.arange(nreq)[:, None] + np.arange(maxs)[None, :] * stride
         if stride > 0 and np.array_equal(slot_array, affine):
             slot_stride = stride
-    # attached segments of each TA_LARGE256 item: count, then (first token, tokens, first job row)
+    # attached segments of each TA_LARGE256 item: count, then (first token, tokens, first job row, rows)
     # (one record per (job, first row), shared by the item of every KV head)
     if attached:
         recs = np.zeros((len(attached), xstride), dtype=np.int32)
         codes = np.zeros(len(attached), dtype=np.int64)
         for i, ((j, row0), segs) in enumerate(attached.items()):
-            rec = [len(segs)] + [x for job, lrow in segs for x in (job.tokens[0], len(job.tokens), lrow)]
-            recs[i, :len(rec)] = rec
+            recs[i, :1 + XTAIL_FIELDS * len(segs)] = _xtail_record(segs, group)
             codes[i] = (j + small_jobs) << 32 | row0
         big = items[_native.TA_LARGE256].reshape(-1, 3).astype(np.int64)
         item_codes = big[:, 0] << 32 | big[:, 1]
@@ -501,7 +517,13 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
                    * kvheads, n_cu, growing)
     attached = {}
     if attach_tails:  # growing tails too: their records' token fields are rewritten by fill_growing
-        small, attached = _attach_tails(small, large, group, tile_rows, lambda job: False)
+        # candidates: the small jobs, then the large ones whose rows fit one wave
+        mids = [j for j in large if len(j.requests) * group <= WAVE_ROWS]
+        left, attached = _attach_tails(small + mids, large, group, tile_rows, lambda job: False)
+        small = [j for j in left if len(j.requests) * group <= SMALL_ROWS]
+        if mids:
+            gone = {id(job) for segs in attached.values() for job, _ in segs}
+            large = [j for j in large if id(j) not in gone]
     # Tails (a request's only small job) stay whole when they alone fill the GPU,
     # so that their work items can merge their requests.
     owners = {}
@@ -514,7 +536,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     jobs = small + large
     small_jobs = len(small)
     njobs = len(jobs)
-    xstride = 1 + 3 * XTAIL_MAX
+    xstride = 1 + XTAIL_FIELDS * XTAIL_MAX
     from . import _planner
     build = _metadata_native if _planner.available() else _metadata_numpy
     meta = build(jobs, small_jobs, nreq, group, kvheads, tile_rows, attached, xstride)
@@ -563,7 +585,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
             big = meta["buf"][offs[k256]:offs[k256 + 1]].reshape(-1, 3)
             for i, (j, row0, _) in enumerate(big.tolist()):
                 for k in slots_of.get((j, row0), ()):
-                    grow.append(int(offs[8]) + i * xstride + 2 + 3 * k)
+                    grow.append(int(offs[8]) + i * xstride + 2 + XTAIL_FIELDS * k)
     grow_offsets = torch.tensor(grow, dtype=torch.long, device=dev) if grow else None
     return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
                         slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t,
