@@ -211,6 +211,14 @@ int ta_decode_append(const void *q, const void *k, const void *v, const void *co
  * under stream capture. */
 int ta_time_next_launch(void *start_event, void *stop_event);
 
+/* Measurement kernel with no counterpart in the reference: a read-only stream
+ * over `bytes` (a multiple of 16) of device memory at `src` (16-byte aligned),
+ * `blocks` workgroups of 256 threads in a grid-stride loop of 16-byte loads,
+ * folding the data into one word per wave, sink[0 .. 4 * blocks).  Its
+ * rate is the read ceiling the memory-bound segment kernels are compared
+ * with.  Launches on `stream` (a hipStream_t). */
+int ta_read_stream(const void *src, int64_t bytes, uint32_t *sink, int32_t blocks, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,7 @@ relative L2 bound of 0.3% against the FP32 oracle evaluated on the same
 import ctypes
 import sys
 
+import numpy as np
 import pytest
 import torch
 
@@ -555,3 +556,20 @@ def test_decode_append_matches_eager_ops(hq, hk, d, shared_rope, dtype, device):
     torch.cuda.synchronize()
     assert torch.equal(out, q_ref[:, :, 0, :].contiguous())
     assert torch.equal(kp, kp_ref) and torch.equal(vp, vp_ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("blocks", [1, 7, 256])
+def test_read_stream_reads_every_byte(blocks, device):
+    """ta_read_stream (the read ceiling of the memory-bound kinds) folds every 16-byte chunk
+    exactly once: the XOR of its per-wave words equals the XOR of all words of the buffer."""
+    lib = _native.load()
+    g = torch.Generator().manual_seed(3)
+    words = torch.randint(-2**31, 2**31 - 1, (1 << 18) + 4 * 37, generator=g, dtype=torch.int64).to(torch.int32)
+    src = words.to(device)
+    sink = torch.zeros(4 * blocks, dtype=torch.int32, device=device)
+    _native.check(lib.ta_read_stream(src.data_ptr(), src.numel() * 4, sink.data_ptr(), blocks,
+                                     torch.cuda.current_stream().cuda_stream))
+    folded = int(np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)))
+    assert folded == int(np.bitwise_xor.reduce(words.numpy().view(np.uint32)))
+    assert lib.ta_read_stream(src.data_ptr(), 12, sink.data_ptr(), blocks, None) == _native.TA_ERR_ARG

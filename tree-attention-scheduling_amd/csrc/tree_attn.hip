@@ -510,6 +510,27 @@ __global__ __launch_bounds__(MERGE_NT) void merge_kernel(const u16 *__restrict__
                           Ops<FP16>::pack(hi[2], hi[3])};
 }
 
+// ------------------------------------------------------------------ read ceiling
+// A read-only stream: every lane loads 16-byte chunks in a grid-stride loop
+// and folds them into one word per wave, the ceiling against which the
+// memory-bound segment kernels are measured (ta_read_stream).
+constexpr int READ_NT = 256;
+
+__global__ __launch_bounds__(READ_NT) void read_stream_kernel(const u32x4 *__restrict__ src, int64_t n,
+                                                              uint32_t *__restrict__ sink) {
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    const int64_t step = (int64_t)gridDim.x * READ_NT;
+    int64_t i = (int64_t)blockIdx.x * READ_NT + threadIdx.x;
+    for (; i + 3 * step < n; i += 4 * step) {
+        const u32x4 a = src[i], b = src[i + step], c = src[i + 2 * step], d = src[i + 3 * step];
+        acc ^= a ^ b ^ c ^ d;
+    }
+    for (; i < n; i += step) acc ^= src[i];
+    uint32_t w = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+    for (int o = 32; o > 0; o >>= 1) w ^= __shfl_xor(w, o);
+    if ((threadIdx.x & 63) == 0) sink[blockIdx.x * (READ_NT / 64) + threadIdx.x / 64] = w;
+}
+
 // ------------------------------------------------------------------ launch
 // resident one-wave workgroups on 256 CUs (8 per CU by LDS at d = 128)
 constexpr int SMALL_MAX_BLOCKS = 2048;
@@ -819,6 +840,14 @@ int ta_attention_matrix_noalloc(const void *q, const void *kp, const void *vp, i
     local.part = base;
     local.lse = reinterpret_cast<float *>(base + lse_offset);
     return attention_layer(q, kp, vp, tcap, &local, out, stream);
+}
+
+int ta_read_stream(const void *src, int64_t bytes, uint32_t *sink, int32_t blocks, void *stream) {
+    if (!src || !sink || bytes <= 0 || bytes % 16 != 0 || blocks <= 0) return TA_ERR_ARG;
+    if (reinterpret_cast<uintptr_t>(src) % 16 != 0) return TA_ERR_ALIGN;
+    TA_LAUNCH(read_stream_kernel, dim3(blocks), dim3(READ_NT), static_cast<hipStream_t>(stream),
+              static_cast<const u32x4 *>(src), bytes / 16, sink);
+    return (int)hipGetLastError();
 }
 
 int ta_time_next_launch(void *start_event, void *stop_event) {

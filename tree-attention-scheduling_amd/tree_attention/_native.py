@@ -18,6 +18,7 @@ LIB_PATH = Path(__file__).with_name("libtree_attn.so")
 TA_BF16, TA_FP16 = 0, 1
 TA_SMALL, TA_LARGE64, TA_LARGE128, TA_LARGE256, TA_TAIL = 0, 1, 2, 3, 4
 TA_NKINDS = 5
+TA_ERR_ARG = 1001
 TA_ERR_SCRATCH = 1004
 NOALLOC_SCRATCH_BYTES = 32 << 20  # TA_NOALLOC_SCRATCH_BYTES
 KIND_ROWS = {TA_LARGE64: 64, TA_LARGE128: 128, TA_LARGE256: 256}
@@ -26,7 +27,8 @@ _c_i32 = ctypes.c_int32
 _c_ptr = ctypes.c_void_p
 
 EXPORTS = ("ta_version", "ta_error_string", "ta_segment", "ta_merge", "ta_attention_matrix",
-           "ta_attention_matrix_noalloc", "ta_tail_merge", "ta_segment_plan", "ta_merge_plan", "ta_decode_append", "ta_time_next_launch")
+           "ta_attention_matrix_noalloc", "ta_tail_merge", "ta_segment_plan", "ta_merge_plan", "ta_decode_append", "ta_time_next_launch",
+           "ta_read_stream")
 
 
 class TaPlan(ctypes.Structure):
@@ -89,6 +91,8 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
                                          _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_ptr]
         lib.ta_time_next_launch.restype = ctypes.c_int
         lib.ta_time_next_launch.argtypes = [_c_ptr, _c_ptr]
+        lib.ta_read_stream.restype = ctypes.c_int
+        lib.ta_read_stream.argtypes = [_c_ptr, ctypes.c_int64, _c_ptr, _c_i32, _c_ptr]
         if path is None:
             _lib = lib
         return lib

@@ -5,9 +5,12 @@
 
 ``--kernel`` is one of ``small``, ``large64``, ``large128``, ``large256``,
 ``tail`` (the tail items writing partials), ``tailmerge`` (the same items
-merging their requests, as in the layer), ``merge``, ``layer`` (the whole attention_matrix call) or ``copy`` (a plain
+merging their requests, as in the layer), ``merge``, ``layer`` (the whole attention_matrix call), ``copy`` (a plain
 device-to-device copy of ``--copy-mib`` MiB, the reference point that scales
-rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes).  K/V rotate over
+rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes) or ``stream`` (the
+library's read-only stream, ``ta_read_stream``, over ``--copy-mib`` MiB: the
+read ceiling of the memory-bound kinds).  With ``--kernel stream`` the row
+also gives the read rate in GB/s.  K/V rotate over
 ``--pools`` copies so repeated launches read HBM, not the MALL.  Prints the
 mean device time per launch measured with HIP events (launch gaps included)
 and, with ``--stamp``, the median of the kernels' own durations (dispatch
@@ -38,7 +41,9 @@ def main(argv=None):
                     help="instead of --shape: R requests on one ROOT-token root with PRIVATE-token tails")
     ap.add_argument("--method", default="cube")
     ap.add_argument("--cost-model", default="mi355x", choices=["mi355x", "reference"])
-    ap.add_argument("--kernel", default="layer", choices=sorted(KINDS) + ["tailmerge", "merge", "layer", "copy"])
+    ap.add_argument("--kernel", default="layer",
+                    choices=sorted(KINDS) + ["tailmerge", "merge", "layer", "copy", "stream"])
+    ap.add_argument("--stream-blocks", type=int, default=4096, help="workgroups of --kernel stream")
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--pools", type=int, default=8)
@@ -85,14 +90,19 @@ def main(argv=None):
         prepared = prepare(plan, q, args.tile_rows)
     attention_matrix(q, kp, vp, prepared)  # partials exist before a lone merge
 
-    if args.kernel == "copy":
+    if args.kernel in ("copy", "stream"):
         src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
+        dst = torch.empty_like(src) if args.kernel == "copy" else torch.zeros(4 * args.stream_blocks,
+                                                                            dtype=torch.int32, device=dev)
+        lib = _native.load()
 
     def launch(i):
         kpi, vpi = pools[i % len(pools)]
         if args.kernel == "copy":
             dst.copy_(src)
+        elif args.kernel == "stream":
+            _native.check(lib.ta_read_stream(src.data_ptr(), src.numel(), dst.data_ptr(), args.stream_blocks,
+                                             torch.cuda.current_stream().cuda_stream))
         elif args.kernel == "layer":
             attention_matrix(q, kpi, vpi, prepared)
         elif args.kernel == "merge":
@@ -117,6 +127,9 @@ def main(argv=None):
            "items": list(prepared.abi.n_items)}
     if args.stamp and args.kernel != "copy":
         row["kernel_us_median"] = statistics.median(launch_durations_us(launch, args.iters))
+    if args.kernel == "stream":
+        row["bytes"] = src.numel()
+        row["read_gbs"] = src.numel() / (row.get("kernel_us_median") or row["us_per_launch"]) / 1e3
     print(json.dumps(row), flush=True)
 
 
