@@ -565,7 +565,7 @@ def test_read_stream_reads_every_byte(blocks, device):
     exactly once: the XOR of its per-wave words equals the XOR of all words of the buffer."""
     lib = _native.load()
     g = torch.Generator().manual_seed(3)
-    words = torch.randint(-2**31, 2**31 - 1, (1 << 18) + 4 * 37, generator=g, dtype=torch.int64).to(torch.int32)
+    words = torch.randint(-2**31, 2**31 - 1, ((1 << 18) + 4 * 37,), generator=g, dtype=torch.int64).to(torch.int32)
     src = words.to(device)
     sink = torch.zeros(4 * blocks, dtype=torch.int32, device=device)
     _native.check(lib.ta_read_stream(src.data_ptr(), src.numel() * 4, sink.data_ptr(), blocks,

@@ -1,0 +1,38 @@
+"""Host logic of the calibration-regret harness (tree_attention/benchmark_regret.py), on CPU."""
+import math
+
+from tree_attention import CostModel, schedule, shapes
+from tree_attention.benchmark_regret import (METHODS, distinct_plans, parameter_sets, plan_key,
+                                             summarize)
+
+
+def test_parameter_sets_hold_the_reference_the_fit_and_the_candidates():
+    sets = parameter_sets()
+    assert sets["reference"] == CostModel()
+    assert sets["fitted"] == CostModel.mi355x()
+    cands = [m for name, m in sets.items() if name.startswith("candidate_")]
+    assert len(cands) == 11 and CostModel.mi355x() not in cands
+    assert {(m.kv_split, m.max_query_rows) for m in cands} | {(512, 512)} >= {(256, 64), (1024, 512)}
+
+
+def test_distinct_plans_cover_every_method_and_set_once():
+    sets = parameter_sets()
+    tree = shapes.tree(shapes.nested_unequal())
+    plans = distinct_plans(tree, sets)
+    keys = [k for k, _, _ in plans]
+    assert len(set(keys)) == len(keys)
+    who = [w for _, _, ws in plans for w in ws]
+    assert sorted(who) == sorted((m, s) for m in METHODS for s in sets)
+    for key, plan, ws in plans:
+        for method, name in ws:
+            assert plan_key(schedule(tree, 32, 8, 128, method, sets[name])) == key
+
+
+def test_summarize():
+    rows = [{"regret": 1.0, "best_by": ("cube", "fitted")}, {"regret": 1.21, "best_by": ("greedy", "reference")},
+            {"regret": 1.01, "best_by": ("cube", "fitted")}]
+    s = summarize(rows)
+    assert math.isclose(s["geomean_regret"], (1.21 * 1.01) ** (1 / 3))
+    assert s["max_regret"] == 1.21 and s["fitted_cube_within_2pct"] == 2
+    assert s["best_by"] == {"cube/fitted": 2, "greedy/reference": 1}
+    assert s["worst"][0]["regret"] == 1.21

@@ -1,0 +1,157 @@
+"""Calibration regret: per evaluation shape, the fastest measured plan over every planning method
+and cost-model parameter set, against the plan the fitted model's subset DP (``cube``) makes.
+
+    python -m tree_attention.benchmark_regret [--grid nested|config|reference|headline]
+        [--iters 10] [--output PATH]
+
+Parameter sets: the reference's Ascend 910B defaults (``CostModel()``, schedule.py:29-39) and
+every candidate of the MI355X calibration -- the continuous terms fitted for each
+``kv_split`` x ``max_query_rows`` pair, ``candidates`` of mi355x_cost_model.json -- among them
+the chosen one (``fitted``).  Methods: request, fixed, greedy, cube (schedule.py:327-458).
+Identical plans are timed once.  Every plan's output is checked against per-request attention in
+fp32 on the device (atol .008 / rtol .03, scripts/benchmark.py:96) before it is timed; timing is
+the mean of ``--iters`` resident ``attention_matrix`` calls between HIP events, rotating over copies
+of the K/V pools that span at least 535 MB.
+
+Per shape: ``fitted_cube_us``, ``best_us`` and the (method, parameter set) that gave it, and
+``regret`` = fitted_cube_us / best_us (1.0 when the fitted DP plan is the fastest measured).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import statistics
+from dataclasses import asdict
+from pathlib import Path
+
+import torch
+
+from . import CostModel, schedule, shapes
+from .calibrate import OUT as FITTED_JSON
+from .harness import check, reference_fp32, rotated_pools
+from .kernels import attention_matrix, pack_kv, prepare
+
+METHODS = ("request", "fixed", "greedy", "cube")
+HQ, HK, D = 32, 8, 128
+
+
+def parameter_sets():
+    """{name: CostModel}: the reference defaults, the fitted model and every calibration candidate."""
+    doc = json.loads(Path(FITTED_JSON).read_text())
+    sets = {"reference": CostModel(), "fitted": CostModel(**doc["params"])}
+    for c in doc["candidates"]:
+        p = c["params"]
+        name = f"candidate_s{p['kv_split']}_q{p['max_query_rows']}"
+        if CostModel(**p) != sets["fitted"]:
+            sets[name] = CostModel(**p)
+    return sets
+
+
+def plan_key(plan):
+    return tuple((j.requests, j.tokens) for j in plan.jobs)
+
+
+def distinct_plans(tree, sets):
+    """[(key, plan, [(method, set name), ...])]: every (method, parameter set) plan, deduplicated."""
+    out = {}
+    for method in METHODS:
+        for name, model in sets.items():
+            plan = schedule(tree, HQ, HK, D, method, model)
+            key = plan_key(plan)
+            if key not in out:
+                out[key] = (plan, [])
+            out[key][1].append((method, name))
+    return [(k, plan, who) for k, (plan, who) in out.items()]
+
+
+def summarize(rows):
+    regrets = [r["regret"] for r in rows]
+    return {"shapes": len(rows),
+            "geomean_regret": math.exp(sum(map(math.log, regrets)) / len(regrets)),
+            "median_regret": statistics.median(regrets), "max_regret": max(regrets),
+            "fitted_cube_within_2pct": sum(x <= 1.02 for x in regrets),
+            "best_by": _count(r["best_by"] for r in rows),
+            "worst": sorted(rows, key=lambda r: -r["regret"])[:5]}
+
+
+def _count(items):
+    out = {}
+    for method, name in items:
+        out[f"{method}/{name}"] = out.get(f"{method}/{name}", 0) + 1
+    return out
+
+
+def _time(q, pools, prepared, iters):
+    for i in range(3):
+        attention_matrix(q, *pools[i % len(pools)], prepared)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(iters):
+        attention_matrix(q, *pools[i % len(pools)], prepared)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / iters
+
+
+def run_shape(params, spec, sets, iters, seed, dev):
+    tree = shapes.tree(spec)
+    g = torch.Generator().manual_seed(seed)
+    t8 = (tree.storage_tokens + 7) // 8 * 8
+    q = torch.randn(len(tree.paths), HQ, D, generator=g).bfloat16().to(dev)
+    k = torch.randn(t8, HK, D, generator=g).bfloat16().to(dev)
+    v = torch.randn(t8, HK, D, generator=g).bfloat16().to(dev)
+    ref = reference_fp32(q, k, v, tree)
+    kp, vp = pack_kv(k, v)
+    del k, v
+    pools = rotated_pools(kp, vp)
+    timed = []
+    for key, plan, who in distinct_plans(tree, sets):
+        prepared = prepare(plan, q)
+        check(attention_matrix(q, kp, vp, prepared), ref, f"{params} {who[0]}")
+        timed.append((_time(q, pools, prepared, iters), key, who))
+    fitted = plan_key(schedule(tree, HQ, HK, D, "cube", sets["fitted"]))
+    fitted_us = next(t for t, key, _ in timed if key == fitted)
+    best_us, _, best_who = min(timed, key=lambda x: x[0])
+    return {"shape": params, "requests": len(tree.paths), "storage_tokens": tree.storage_tokens,
+            "fitted_cube_us": fitted_us, "best_us": best_us, "best_by": best_who[0],
+            "best_also": best_who[1:], "regret": fitted_us / best_us, "distinct_plans": len(timed),
+            "plans": [{"us": t, "by": who} for t, _, who in sorted(timed, key=lambda x: x[0])]}
+
+
+def grid_of(name):
+    if name == "nested":
+        return [({"tree": "nested_unequal"}, shapes.nested_unequal())]
+    if name == "headline":
+        return [({"tree": "headline"}, shapes.headline())]
+    return list(shapes.config_grid() if name == "config" else shapes.reference_grid())
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--grid", default="nested", choices=["nested", "config", "reference", "headline"])
+    ap.add_argument("--iters", type=int, default=10)
+    ap.add_argument("--seed", type=int, default=201)
+    ap.add_argument("--limit", type=int, default=0, help="run only the first N shapes")
+    ap.add_argument("--output", default=None)
+    args = ap.parse_args(argv)
+    dev = torch.device("cuda:0")
+    sets = parameter_sets()
+    grid = grid_of(args.grid)[:args.limit or None]
+    run_shape(*grid[0], {"fitted": sets["fitted"]}, 1, args.seed, dev)  # untimed: first loads and calls
+    rows = []
+    for params, spec in grid:
+        row = run_shape(params, spec, sets, args.iters, args.seed, dev)
+        print(json.dumps({k: v for k, v in row.items() if k != "plans"}), flush=True)
+        rows.append(row)
+    doc = {"grid": args.grid, "device": torch.cuda.get_device_name(0),
+           "parameter_sets": {k: asdict(v) for k, v in sets.items()},
+           "summary": summarize(rows), "rows": rows}
+    print(json.dumps({"summary": {k: v for k, v in doc["summary"].items() if k != "worst"}}), flush=True)
+    if args.output:
+        Path(args.output).write_text(json.dumps(doc, indent=1) + "\n")
+
+
+if __name__ == "__main__":
+    main()
