@@ -351,7 +351,7 @@ def test_tail_items_with_merge_rest(dtype, device):
     v = torch.randn(528, 4, 128, generator=g).to(dtype)
     qd = q.to(device)
     kp, vp = pack_kv(k.to(device), v.to(device))
-    prepared = prepare(Plan(jobs, "x", 0.0, dict(kvheads=4)), qd)
+    prepared = prepare(Plan(jobs, "x", 0.0, dict(kvheads=4)), qd, route_items=0)  # the large job stays large
     tails = {prepared.jobs[j].requests for j, _, _ in prepared.items[_native.TA_TAIL].view(-1, 3).tolist()}
     assert tails == {(0,)} and prepared.rest.tolist() == [1, 2, 3, 4, 5]
     out = attention_matrix(qd, kp, vp, prepared)

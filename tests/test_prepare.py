@@ -137,7 +137,7 @@ def test_tail_items_and_merge_rest():
             Job((0,), tuple(range(40, 50))), Job((1,), tuple(range(50, 60))),
             Job((2, 3), tuple(range(64, 70))), Job((1,), tuple(range(70, 74)))]
     q = torch.empty(6, 8, 32, dtype=torch.float16)
-    p = prepare(Plan(jobs, "x", 0.0, settings), q)
+    p = prepare(Plan(jobs, "x", 0.0, settings), q, route_items=0)  # the large job stays large
     tail_jobs = sorted({j for j, _, _ in p.items[_native.TA_TAIL].view(-1, 3).tolist()})
     assert [p.jobs[j].requests for j in tail_jobs] == [(0,)]
     # request 1 has two small jobs, 2 and 3 share one, 4 and 5 have only the large job
@@ -184,18 +184,31 @@ def test_private_tails_attach_to_root_items():
 
 def test_attachment_limits():
     """Tails attach only where the request's rows fit one wave, up to XTAIL_MAX segments and
-    the item's own tile count (at least ATTACH_MIN_CAP tiles); growing decode tails attach
-    too, their lengths rewritten in the attachment records by fill_growing."""
+    the item's own tile count -- at least ATTACH_MIN_CAP tiles when every candidate attaches
+    (the layer then has no small-job launch), exactly its own when some stay small jobs;
+    growing decode tails attach too, their lengths rewritten in the attachment records by
+    fill_growing."""
     settings = dict(kvheads=1)
     q = torch.empty(80, 4, 32, dtype=torch.float16)   # group 4: 80 requests = 320 rows
     root = Job(tuple(range(80)), tuple(range(0, 64)))  # one tile of root tokens
     tails = [Job((r,), tuple(range(64 + 16 * r, 80 + 16 * r))) for r in range(80)]
-    p = prepare(Plan([root] + tails, "x", 0.0, settings), q)
     # two row tiles (rows 0-255, 256-319) of one job, one own tile each: each takes
     # XTAIL_MAX one-tile tails (within the ATTACH_MIN_CAP floor of attached tiles)
     assert kernels.XTAIL_MAX <= kernels.ATTACH_MIN_CAP
+    left, att = kernels._attach_tails(tails, [root], 4, 256, lambda job: False)
+    assert sorted((j, row0, len(s)) for (j, row0), s in att.items()) == [
+        (0, 0, kernels.XTAIL_MAX), (0, 256, kernels.XTAIL_MAX)]
+    assert len(left) == 80 - 2 * kernels.XTAIL_MAX
+    # when every candidate fits, prepare attaches them all that way: one segment launch
+    few = [t for t in tails if t.requests[0] % 64 < kernels.XTAIL_MAX]
+    p = prepare(Plan([root] + few, "x", 0.0, settings), q)
+    assert p.small_jobs == 0 and len(p.jobs) == 1
     assert sorted((j, row0, len(s)) for (j, row0), s in p.attached.items()) == [
-        (p.small_jobs, 0, kernels.XTAIL_MAX), (p.small_jobs, 256, kernels.XTAIL_MAX)]
+        (0, 0, kernels.XTAIL_MAX), (0, 256, kernels.XTAIL_MAX)]
+    # with tails left for the small-job kernel, an item takes no more tiles than its own (one)
+    p = prepare(Plan([root] + tails, "x", 0.0, settings), q, route_items=0)
+    assert sorted((j, row0, len(s)) for (j, row0), s in p.attached.items()) == [
+        (p.small_jobs, 0, 1), (p.small_jobs, 256, 1)]
     assert len(p.jobs) == p.small_jobs + 1
     tree_paths = [tuple(range(0, 64)) + tuple(range(64 + 16 * r, 80 + 16 * r)) for r in range(80)]
     seen = [[] for _ in range(80)]
@@ -208,24 +221,27 @@ def test_attachment_limits():
     assert all(sorted(seen[r]) == list(tree_paths[r]) for r in range(80))
     # growing tails (fixed_from) attach the same way; fill_growing sets the klen of those
     # left as jobs and the token field of every record holding an attached one
-    g = prepare(Plan([root] + tails, "x", 0.0, settings), q, fixed_from=64)
+    g = prepare(Plan([root] + few, "x", 0.0, settings), q, fixed_from=64)
+    assert g.small_jobs == 0 and g.grow_offsets.numel() == 2 * kernels.XTAIL_MAX
+    g = prepare(Plan([root] + tails, "x", 0.0, settings), q, fixed_from=64, route_items=0)
     assert {k: [(j.requests, lr) for j, lr in v] for k, v in g.attached.items()} == \
         {k: [(j.requests, lr) for j, lr in v] for k, v in p.attached.items()}
     njob_tails = sum(job.tokens[0] >= 64 for job in g.jobs)
-    assert njob_tails == 80 - 2 * kernels.XTAIL_MAX
-    assert g.grow_offsets.numel() == njob_tails + 2 * kernels.XTAIL_MAX
+    assert njob_tails == 80 - 2
+    assert g.grow_offsets.numel() == njob_tails + 2
     g.fill_growing(3)
     assert (g.klen[torch.tensor([j.tokens[0] >= 64 for j in g.jobs])] == 3).all()
     recs = g.xtail.view(-1, 1 + 4 * kernels.XTAIL_MAX)
-    assert (recs[:, 0] == kernels.XTAIL_MAX).all()
-    assert (recs[:, 2:1 + 4 * kernels.XTAIL_MAX:4] == 3).all()  # every attached segment's token count
-    assert (recs[:, 4:1 + 4 * kernels.XTAIL_MAX:4] == 4).all()  # and its rows (one request, group 4)
+    assert (recs[:, 0] == 1).all()
+    assert (recs[:, 2] == 3).all()  # every attached segment's token count
+    assert (recs[:, 4] == 4).all()  # and its rows (one request, group 4)
     g.fill_growing(16)
-    assert (recs[:, 2:1 + 4 * kernels.XTAIL_MAX:4] == 16).all() and (g.klen[-1] == 64).all()
+    assert (recs[:, 2] == 16).all() and (g.klen[-1] == 64).all()
     # group 12: request 1's rows 12-23 lie in wave 0; request 2's rows 24-35 straddle waves 0 and 1
     q = torch.empty(24, 12, 32, dtype=torch.float16)
     root = Job(tuple(range(24)), tuple(range(0, 256)))
-    p = prepare(Plan([root, Job((1,), (300, 301)), Job((2,), (302, 303))], "x", 0.0, settings), q)
+    p = prepare(Plan([root, Job((1,), (300, 301)), Job((2,), (302, 303))], "x", 0.0, settings), q,
+                route_items=0)
     assert [(job.requests, lrow) for segs in p.attached.values() for job, lrow in segs] == [((1,), 12)]
     assert [job.requests for job in p.jobs[:p.small_jobs]] == [(2,)]
 
@@ -259,7 +275,7 @@ def test_nodes_of_a_wave_attach():
     root = Job(tuple(range(32)), tuple(range(0, 512)))
     branches = [Job(tuple(range(8 * b, 8 * b + 8)), tuple(range(512 + 64 * b, 576 + 64 * b))) for b in range(4)]
     misaligned = Job(tuple(range(4, 12)), tuple(range(800, 864)))    # rows 16-47: two waves
-    gapped = Job((1, 3), tuple(range(900, 932)))                       # rows 4-7 and 12-15: not consecutive
+    gapped = Job((1, 3, 5, 7, 9), tuple(range(900, 932)))              # rows 4-7, 12-15, ...: not consecutive
     # root: 8 one-tile items of 4 segments each; 16 tails leave room for the nodes
     tails = [Job((r,), tuple(range(1000 + 16 * r, 1016 + 16 * r))) for r in range(0, 32, 2)]
     plan = Plan([root] + branches + [misaligned, gapped] + tails, "x", 0.0, settings)
@@ -306,3 +322,28 @@ def _covers_paths_plan(p, plan, nreq):
             for r in job.requests:
                 seen[r].extend(job.tokens)
     return all(sorted(seen[r]) == sorted(want[r]) for r in range(nreq))
+
+
+def test_small_large_jobs_run_in_the_small_kernel():
+    """When small jobs are left for the small-job kernel and the large jobs, cut into 16-row
+    request groups, stream at most route_items (tile, KV head) units, the large jobs run as
+    those groups in the small-job kernel: one segment launch, the same tokens per request.
+    Above the limit, or when every small job attaches (no small-job launch), they stay large."""
+    settings = dict(kvheads=2)
+    q = torch.empty(32, 8, 32, dtype=torch.float16)   # group 4: 4 requests per 16-row group
+    root = Job(tuple(range(32)), tuple(range(0, 256)))                      # 8 groups x 4 tiles
+    tails = [Job((r,), tuple(range(256 + 768 * r, 256 + 768 * (r + 1)))) for r in range(32)]  # 12 tiles each
+    plan = Plan([root] + tails, "x", 0.0, settings)
+    p = prepare(plan, q)   # 8 groups x 4 tiles x 2 KV heads = 64 units
+    assert len(p.jobs) == p.small_jobs and p.abi.n_items[_native.TA_LARGE256] == 0 and not p.attached
+    assert sorted({job.requests for job in p.jobs if job.tokens[0] < 256}) == \
+        [tuple(range(i, i + 4)) for i in range(0, 32, 4)]
+    assert _covers_paths_plan(p, plan, 32)
+    for limit, routed in ((0, False), (63, False), (64, True)):
+        r = prepare(plan, q, route_items=limit)
+        assert (r.small_jobs == len(r.jobs)) == routed and _covers_paths_plan(r, plan, 32)
+    # one-token tails that all attach (the root's four 64-token chunks take four each): no
+    # small-job launch to share, no routing
+    short = [Job((r,), (256 + r,)) for r in range(16)]
+    a = prepare(Plan([root] + short, "x", 0.0, settings), q)
+    assert a.small_jobs == 0 and sum(map(len, a.attached.values())) == 16

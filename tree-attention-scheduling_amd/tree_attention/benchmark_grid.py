@@ -2,7 +2,7 @@
 and the comparison block of scripts/analyze_planning.py:60-64).
 
     python -m tree_attention.benchmark_grid [--grid config|reference|nested] [--iters 10]
-        [--cost-model mi355x|reference] [--output PATH]
+        [--cost-model mi355x|reference] [--route-items N] [--output PATH]
 
 ``--grid config`` (default) is the 81-shape requests x context x shared fraction x
 depth factorial of ``shapes.config_grid``; ``--grid reference`` is the reference's own
@@ -23,6 +23,8 @@ method's output is checked before it is timed, here against
 reference's device tolerance atol .008 / rtol .03; ``max_abs_error`` and
 ``rel_l2`` are recorded.  The CPU oracle comparison of the same shapes is the GPU
 test suite's (tests/test_gpu_configs.py).
+``--route-items`` sets ``prepare``'s limit for running large jobs in the small-job kernel
+(default ``kernels.ROUTE_ITEMS``; 0 never routes).
 ``comparisons`` holds, per baseline method and metric, the geometric-mean speedup of
 ``cube`` over it, as scripts/analyze_planning.py:60-64 computes it.
 """
@@ -39,7 +41,7 @@ import torch
 
 from . import CostModel, schedule, shapes
 from .harness import check, pool_bytes, reference_fp32, rotated_pools
-from .kernels import attention_matrix, pack_kv, prepare
+from .kernels import ROUTE_ITEMS, attention_matrix, pack_kv, prepare
 
 METHODS = ("request", "fixed", "greedy", "cube")
 HQ, HK, D = 32, 8, 128
@@ -58,7 +60,7 @@ def _time_layer(q, pools, prepared, iters):
     return start.elapsed_time(end) * 1e3 / iters
 
 
-def run_shape(params, spec, model, iters, seed, dev, log):
+def run_shape(params, spec, model, iters, seed, dev, log, route_items=ROUTE_ITEMS):
     tree = shapes.tree(spec)
     g = torch.Generator().manual_seed(seed)
     t8 = (tree.storage_tokens + 7) // 8 * 8
@@ -77,7 +79,7 @@ def run_shape(params, spec, model, iters, seed, dev, log):
         plan.validate(tree)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        prepared = prepare(plan, q)
+        prepared = prepare(plan, q, route_items=route_items)
         torch.cuda.synchronize()
         metadata_us = (time.perf_counter() - t0) * 1e6
         err = check(attention_matrix(q, kp, vp, prepared), ref, f"{params} {method}")
@@ -116,6 +118,7 @@ def main(argv=None):
     ap.add_argument("--seed", type=int, default=201)
     ap.add_argument("--cost-model", default="mi355x", choices=["mi355x", "reference"])
     ap.add_argument("--limit", type=int, default=0, help="run only the first N shapes")
+    ap.add_argument("--route-items", type=int, default=ROUTE_ITEMS)
     ap.add_argument("--output", default=None)
     args = ap.parse_args(argv)
     dev = torch.device("cuda:0")
@@ -130,8 +133,10 @@ def main(argv=None):
     run_shape(*grid[0], model, 1, args.seed, dev, lambda s: None)
     rows = []
     for params, spec in grid:
-        rows += run_shape(params, spec, model, args.iters, args.seed, dev, lambda s: print(s, flush=True))
-    doc = {"grid": args.grid, "cost_model": args.cost_model, "device": torch.cuda.get_device_name(0),
+        rows += run_shape(params, spec, model, args.iters, args.seed, dev, lambda s: print(s, flush=True),
+                          args.route_items)
+    doc = {"grid": args.grid, "cost_model": args.cost_model, "route_items": args.route_items,
+           "device": torch.cuda.get_device_name(0),
            "rows": rows, "comparisons": comparisons(rows)}
     print(json.dumps({"comparisons": doc["comparisons"]}), flush=True)
     if args.output:

@@ -180,6 +180,11 @@ WAVE_ROWS = 32      # query rows of one wave of the TA_LARGE256 kernel
 # attached tiles an item may take beyond its own count: the one-tile root items of
 # decode-sized layers take their requests' private and growing tails
 ATTACH_MIN_CAP = 2 * XTAIL_MAX
+# large jobs run in the small-job kernel as 16-row request groups when the small-job
+# kernel launches anyway and the groups stream at most this many (tile, KV head) work
+# units: about 0.4 tile per resident small-job wave (8 per CU), less than the start-up
+# of a launch of its own (measured over the 81-shape evaluation grid)
+ROUTE_ITEMS = 768
 
 
 def _tiles(job) -> int:
@@ -188,7 +193,7 @@ def _tiles(job) -> int:
     return -(-(t0 + len(job.tokens) - (t0 & ~7)) // TOKEN_QUANTUM)
 
 
-def _attach_tails(small, large, group, tile_rows, is_fixed):
+def _attach_tails(small, large, group, tile_rows, is_fixed, min_cap=ATTACH_MIN_CAP):
     """``_attach_tails_py`` through the host library (``tp_attach_tails``) when it is built.
     ``small`` are the candidate jobs (any job whose rows fit one wave).
 
@@ -196,14 +201,14 @@ def _attach_tails(small, large, group, tile_rows, is_fixed):
     """
     from . import _planner
     if not small or not large or not _planner.available():
-        return _attach_tails_py(small, large, group, tile_rows, is_fixed)
+        return _attach_tails_py(small, large, group, tile_rows, is_fixed, min_cap)
     is256 = [_large_kind(len(j.requests) * group, tile_rows) == _native.TA_LARGE256 for j in large]
     if not any(is256):
         return small, {}
     nreq = 1 + max(max(j.requests) for j in (*large, *small))
     item, lrow, keys = _planner.attach_tails(
         large, small, group, is256, [_tiles(j) for j in large], [_tiles(j) for j in small],
-        [bool(is_fixed(j)) for j in small], nreq, XTAIL_MAX, WAVE_ROWS, 256, ATTACH_MIN_CAP)
+        [bool(is_fixed(j)) for j in small], nreq, XTAIL_MAX, WAVE_ROWS, 256, min_cap)
     attached, left = {}, []
     for job, it, lr in zip(small, item, lrow):
         if it < 0:
@@ -213,7 +218,7 @@ def _attach_tails(small, large, group, tile_rows, is_fixed):
     return left, attached
 
 
-def _attach_tails_py(small, large, group, tile_rows, is_fixed):
+def _attach_tails_py(small, large, group, tile_rows, is_fixed, min_cap=ATTACH_MIN_CAP):
     """Fold jobs whose rows fit one wave into TA_LARGE256 work items of large jobs.
 
     A candidate job over requests ``r0 .. rn-1`` (a private tail, or a node of
@@ -225,7 +230,7 @@ def _attach_tails_py(small, large, group, tile_rows, is_fixed):
     goes to the candidate item with the fewest attached tiles (then the fewest
     on the owning wave, then the first large job), up to ``XTAIL_MAX``
     segments per item and no more attached tiles than the item's own (at least
-    ``ATTACH_MIN_CAP``), so the large kernel's items stay balanced.  Jobs for
+    ``min_cap``), so the large kernel's items stay balanced.  Jobs for
     which ``is_fixed`` holds are not attached.  A growing decode tail is
     balanced by its reserved length; its record reads the current length on
     the device.
@@ -273,7 +278,7 @@ def _attach_tails_py(small, large, group, tile_rows, is_fixed):
             if len(job.requests) > 1 and not fits(J, lrow, job.requests):
                 continue
             t = item_tiles[item]
-            if item_segs[item] >= XTAIL_MAX or t + n > max(own[item], ATTACH_MIN_CAP):
+            if item_segs[item] >= XTAIL_MAX or t + n > max(own[item], min_cap):
                 continue
             score = (t, wave_tiles[item * waves + wave], J)
             if best is None or score < best[0]:
@@ -474,7 +479,7 @@ def _metadata_numpy(jobs, small_jobs, nreq, group, kvheads, tile_rows, attached,
 
 
 def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int | None = None,
-            attach_tails: bool = True) -> PreparedPlan:
+            attach_tails: bool = True, route_items: int = ROUTE_ITEMS) -> PreparedPlan:
     """Lower ``plan`` to device metadata and scratch for queries shaped like ``q``.
 
     Mirrors kernels.py:103-141: physical jobs, stable small-first order, one
@@ -486,7 +491,10 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     start at or after it (decode tails whose length changes) as they are.
     ``attach_tails`` folds private single-request jobs into the 256-row work
     items of the large jobs holding their request (``_attach_tails``); those
-    tails are then in ``attached``, not in ``jobs``.  Raises
+    tails are then in ``attached``, not in ``jobs``.  When small jobs are left for
+    the small-job kernel and the large jobs, cut into 16-row request groups, stream
+    at most ``route_items`` (tile, KV head) units, the large jobs run as those
+    groups in the small-job kernel instead (one segment launch less).  Raises
     ``ValueError`` for jobs without requests or tokens, request ids outside
     ``q`` and token runs that are not consecutive physical ids.
     """
@@ -508,6 +516,10 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
         raise ValueError("Plan has no jobs")
     small = [j for j in jobs if len(j.requests) * group <= SMALL_ROWS]
     large = [j for j in jobs if len(j.requests) * group > SMALL_ROWS]
+    per = SMALL_ROWS // group
+    routed = [Job(j.requests[i:i + per], j.tokens) for j in large for i in range(0, len(j.requests), per)] \
+        if per and small and large else []
+    small0 = small
     n_cu = _cu_count(q.device)
 
     def growing(job):
@@ -520,10 +532,16 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
         # candidates: the small jobs, then the large ones whose rows fit one wave
         mids = [j for j in large if len(j.requests) * group <= WAVE_ROWS]
         left, attached = _attach_tails(small + mids, large, group, tile_rows, lambda job: False)
+        if any(len(j.requests) * group <= SMALL_ROWS for j in left):
+            # the small-job kernel launches anyway: items take no more attached tiles than
+            # their own, so that the large kernel does not become the longer of the two
+            left, attached = _attach_tails(small + mids, large, group, tile_rows, lambda job: False, 0)
         small = [j for j in left if len(j.requests) * group <= SMALL_ROWS]
         if mids:
             gone = {id(job) for segs in attached.values() for job, _ in segs}
             large = [j for j in large if id(j) not in gone]
+    if small and routed and sum(map(_tiles, routed)) * kvheads <= route_items:
+        small, large, attached = small0 + routed, [], {}
     # Tails (a request's only small job) stay whole when they alone fill the GPU,
     # so that their work items can merge their requests.
     owners = {}
@@ -590,7 +608,8 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
                         slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t,
                         keyed, xtail_t if attached else None, plan,
-                        {"tile_rows": tile_rows, "fixed_from": fixed_from}, None, meta["qbase"].tolist(),
+                        {"tile_rows": tile_rows, "fixed_from": fixed_from, "route_items": route_items}, None,
+                        meta["qbase"].tolist(),
                         grow_offsets=grow_offsets)
 
 
