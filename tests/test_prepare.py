@@ -23,7 +23,7 @@ def _covers_paths(prepared, tree):
 def test_metadata_layout_small_first_and_compact_slots():
     tree = shapes.tree(shapes.headline())
     q = torch.empty(128, 32, 128, dtype=torch.bfloat16)
-    p = prepare(schedule(tree, 32, 8, 128, "cube"), q)
+    p = prepare(schedule(tree, 32, 8, 128, "cube"), q, fuse_rows=0)
     # default model: 16-request groups x 512-token chunks of the root; each group's
     # chunks are re-cut into 4 chunks of 2032 tokens (8 groups x 4 x 8 heads = 256
     # one-tile workgroups), the 128 private tails stay small jobs
@@ -151,7 +151,8 @@ def test_private_tails_attach_to_root_items():
     tree = shapes.tree(shapes.headline())
     q = torch.empty(128, 32, 128, dtype=torch.bfloat16)
     p = prepare(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q)
-    assert p.small_jobs == 0 and len(p.jobs) == 16
+    # the root in 16 chunks over all 128 requests (request groups of one chunk fuse)
+    assert p.small_jobs == 0 and len(p.jobs) == 16 and {len(j.requests) for j in p.jobs} == {128}
     assert _covers_paths(p, tree)
     assert p.abi.n_items[_native.TA_TAIL] == 0 and p.abi.n_items[_native.TA_SMALL] == 0
     assert p.counts.tolist() == [16] * 128 and p.abi.n_rest == 128
@@ -347,3 +348,32 @@ def test_small_large_jobs_run_in_the_small_kernel():
     short = [Job((r,), (256 + r,)) for r in range(16)]
     a = prepare(Plan([root] + short, "x", 0.0, settings), q)
     assert a.small_jobs == 0 and sum(map(len, a.attached.values())) == 16
+
+
+def test_jobs_over_one_token_run_fuse():
+    """Jobs over the same token run that together hold at least fuse_rows query rows and share
+    no request run as one job over their requests: the headline under the reference's cost
+    model (16-request groups of each 512-token root chunk) runs as 128-request chunks in the
+    256-row kernel, with the slots of the 128-request plan.  Below the row count, or when two
+    jobs share a request, they stay apart."""
+    tree = shapes.tree(shapes.headline())
+    q = torch.empty(128, 32, 128, dtype=torch.bfloat16)
+    plan = schedule(tree, 32, 8, 128, "cube")
+    assert {len(j.requests) for j in plan.jobs} == {1, 16}
+    p = prepare(plan, q)
+    assert {len(j.requests) for j in p.jobs[p.small_jobs:]} == {128}
+    assert p.abi.n_items[_native.TA_LARGE256] == 256 and p.abi.n_items[_native.TA_LARGE64] == 0
+    assert _covers_paths(p, tree)
+    assert p.abi.slot_stride == 128
+    settings = dict(kvheads=1)
+    q = torch.empty(40, 4, 32, dtype=torch.float16)
+    a, b = Job(tuple(range(0, 20)), tuple(range(0, 64))), Job(tuple(range(20, 40)), tuple(range(0, 64)))
+    c = Job(tuple(range(0, 40)), tuple(range(64, 128)))
+    fused = prepare(Plan([a, b, c], "x", 0.0, settings), q, fuse_rows=160)
+    assert sorted(j.requests for j in fused.jobs) == [tuple(range(40))] * 2
+    apart = prepare(Plan([a, b, c], "x", 0.0, settings), q, fuse_rows=161)
+    assert sorted(len(j.requests) for j in apart.jobs) == [20, 20, 40]
+    shared = Job(tuple(range(19, 39)), tuple(range(0, 64)))   # request 19 in both
+    q2 = torch.empty(39, 4, 32, dtype=torch.float16)
+    kept = prepare(Plan([a, shared, Job((39 - 1,), (200,))], "x", 0.0, settings), q2, fuse_rows=1)
+    assert sorted(len(j.requests) for j in kept.jobs if j.tokens[0] == 0) == [20, 20]

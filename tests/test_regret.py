@@ -12,7 +12,11 @@ def test_parameter_sets_hold_the_reference_the_fit_and_the_candidates():
     assert sets["fitted"] == CostModel.mi355x()
     cands = [m for name, m in sets.items() if name.startswith("candidate_")]
     assert len(cands) == 11 and CostModel.mi355x() not in cands
-    assert {(m.kv_split, m.max_query_rows) for m in cands} | {(512, 512)} >= {(256, 64), (1024, 512)}
+    lsq = [m for name, m in sets.items() if name.startswith("least_squares_")]
+    assert lsq and all(m not in cands for m in lsq)
+    fitted = CostModel.mi355x()
+    pairs = {(m.kv_split, m.max_query_rows) for m in cands} | {(fitted.kv_split, fitted.max_query_rows)}
+    assert pairs == {(s, r) for s in (256, 512, 1024) for r in (64, 128, 256, 512)}
 
 
 def test_distinct_plans_cover_every_method_and_set_once():

@@ -5,9 +5,9 @@ and cost-model parameter set, against the plan the fitted model's subset DP (``c
         [--iters 10] [--output PATH]
 
 Parameter sets: the reference's Ascend 910B defaults (``CostModel()``, schedule.py:29-39) and
-every candidate of the MI355X calibration -- the continuous terms fitted for each
+every candidate of the MI355X calibration -- the continuous terms tuned for each
 ``kv_split`` x ``max_query_rows`` pair, ``candidates`` of mi355x_cost_model.json -- among them
-the chosen one (``fitted``).  Methods: request, fixed, greedy, cube (schedule.py:327-458).
+the chosen one (``fitted``), and each candidate's least-squares terms before the tuning.  Methods: request, fixed, greedy, cube (schedule.py:327-458).
 Identical plans are timed once.  Every plan's output is checked against per-request attention in
 fp32 on the device (atol .008 / rtol .03, scripts/benchmark.py:96) before it is timed; timing is
 the mean of ``--iters`` resident ``attention_matrix`` calls between HIP events, rotating over copies
@@ -45,6 +45,9 @@ def parameter_sets():
         name = f"candidate_s{p['kv_split']}_q{p['max_query_rows']}"
         if CostModel(**p) != sets["fitted"]:
             sets[name] = CostModel(**p)
+        lsq = c.get("least_squares_params")
+        if lsq and CostModel(**lsq) not in sets.values():
+            sets["least_squares_" + name[len("candidate_"):]] = CostModel(**lsq)
     return sets
 
 

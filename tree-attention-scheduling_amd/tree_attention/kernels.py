@@ -185,6 +185,8 @@ ATTACH_MIN_CAP = 2 * XTAIL_MAX
 # units: about 0.4 tile per resident small-job wave (8 per CU), less than the start-up
 # of a launch of its own (measured over the 81-shape evaluation grid)
 ROUTE_ITEMS = 768
+# jobs over one token run execute as one job when together they fill a 256-row work item
+FUSE_ROWS = 256
 
 
 def _tiles(job) -> int:
@@ -292,6 +294,38 @@ def _attach_tails_py(small, large, group, tile_rows, is_fixed, min_cap=ATTACH_MI
         item_segs[item] += 1
         wave_tiles[item * waves + wave] += n
     return left, attached
+
+
+def _fuse_same_tokens(jobs, group, min_rows):
+    """Jobs over the same token run run as one job over the union of their requests when
+    together they hold at least ``min_rows`` query rows and share no request.
+
+    Each request keeps one partial over those tokens, so the attention is the same; the K/V
+    run is streamed once per 256-row work item instead of once per job.  A plan that splits
+    a wide node into request groups (a cost model with 64-row query tiles) then runs the node
+    in the 256-row kernel.  The fused job takes the place of the first of its jobs.
+    """
+    runs = {}
+    for j in jobs:
+        runs.setdefault((j.tokens[0], len(j.tokens)), []).append(j)
+    fused = {}
+    for key, grp in runs.items():
+        if len(grp) < 2:
+            continue
+        reqs = [r for j in grp for r in j.requests]
+        if len(reqs) * group >= min_rows and len(set(reqs)) == len(reqs):
+            fused[key] = Job(tuple(sorted(reqs)), grp[0].tokens)
+    if not fused:
+        return jobs
+    out = []
+    for j in jobs:
+        key = (j.tokens[0], len(j.tokens))
+        if key not in fused:
+            out.append(j)
+        elif fused[key] is not None:
+            out.append(fused[key])
+            fused[key] = None
+    return out
 
 
 def _recut(jobs, items_per_chunk, target_items, is_fixed):
@@ -479,15 +513,16 @@ def _metadata_numpy(jobs, small_jobs, nreq, group, kvheads, tile_rows, attached,
 
 
 def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int | None = None,
-            attach_tails: bool = True, route_items: int = ROUTE_ITEMS) -> PreparedPlan:
+            attach_tails: bool = True, route_items: int = ROUTE_ITEMS, fuse_rows: int = FUSE_ROWS) -> PreparedPlan:
     """Lower ``plan`` to device metadata and scratch for queries shaped like ``q``.
 
     Mirrors kernels.py:103-141: physical jobs, stable small-first order, one
     host-to-device copy of all int32 metadata, scratch allocated once.
     ``tile_rows`` (64, 128 or 256) caps the query rows one workgroup of the
     large-job kernels handles; it changes the work split, not the result.
-    Runs of jobs over one request group are re-cut for the GPU (``_recut``), so
-    ``jobs`` holds the execution jobs; ``fixed_from`` keeps jobs whose tokens
+    Jobs over the same token run that together hold at least ``fuse_rows`` query
+    rows (0: never) run as one (``_fuse_same_tokens``).  Runs of jobs over one request group are re-cut for the
+    GPU (``_recut``), so ``jobs`` holds the execution jobs; ``fixed_from`` keeps jobs whose tokens
     start at or after it (decode tails whose length changes) as they are.
     ``attach_tails`` folds private single-request jobs into the 256-row work
     items of the large jobs holding their request (``_attach_tails``); those
@@ -514,6 +549,8 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
             raise ValueError(f"Job {i} tokens are not one run of consecutive physical ids")
     if not jobs:
         raise ValueError("Plan has no jobs")
+    if fuse_rows > 0:
+        jobs = _fuse_same_tokens(jobs, group, fuse_rows)
     small = [j for j in jobs if len(j.requests) * group <= SMALL_ROWS]
     large = [j for j in jobs if len(j.requests) * group > SMALL_ROWS]
     per = SMALL_ROWS // group
@@ -527,6 +564,9 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
 
     large = _recut(large, lambda r: -(-len(r) * group // _native.KIND_ROWS[_large_kind(len(r) * group, tile_rows)])
                    * kvheads, n_cu, growing)
+    # chunks of one token range side by side: a root split into request groups then gives
+    # request r its k-th slot at r + k * (requests of a chunk), the layout the merge computes
+    large.sort(key=lambda j: (j.tokens[0], j.requests[0]))
     attached = {}
     if attach_tails:  # growing tails too: their records' token fields are rewritten by fill_growing
         # candidates: the small jobs, then the large ones whose rows fit one wave
@@ -608,7 +648,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
                         slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t,
                         keyed, xtail_t if attached else None, plan,
-                        {"tile_rows": tile_rows, "fixed_from": fixed_from, "route_items": route_items}, None,
+                        {"tile_rows": tile_rows, "fixed_from": fixed_from, "route_items": route_items, "fuse_rows": fuse_rows}, None,
                         meta["qbase"].tolist(),
                         grow_offsets=grow_offsets)
 

@@ -141,6 +141,25 @@ def calibration_grid():
         parents.append(1 + leaf % 2)
         lengths.append((73, 79, 91)[leaf % 3])
     yield "two_level_r60", (parents, lengths, list(range(3, 63)))
+    # three levels with unequal branches, a request ending at an inner node and a duplicate
+    # path: request counts whose rows are not a multiple of the 256-row tile
+    for name, root, mids, leaves_per, mid_len, leaf_len in (("nested_r26", 3700, 3, 8, 905, 230),
+                                                            ("nested_r54", 2600, 4, 13, 1300, 170)):
+        parents, lengths, terminals = [-1], [root], []
+        for m in range(mids):
+            node = len(parents)
+            parents.append(0)
+            lengths.append(mid_len + 11 * m)
+            for _ in range(leaves_per):
+                terminals.append(len(parents))
+                parents.append(node)
+                lengths.append(leaf_len)
+        yield name, (parents, lengths, terminals + [1, terminals[0]])
+    # deeper trees in the evaluation grid's form (balanced binary splits of the shared part),
+    # at request counts and lengths of their own
+    for requests, context, fraction, depth in product((20, 40, 96), (1500, 6000), (0.5, 0.9), (2, 3)):
+        yield (f"deep_r{requests}_{context}_{int(fraction * 100)}_d{depth}",
+               grid_tree(requests, context, fraction, depth))
 
 
 def qwen3_4b_workload(seed: int = 5) -> list:
