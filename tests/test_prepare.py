@@ -16,7 +16,8 @@ def _covers_paths(prepared, tree):
             seen[r].extend(job.tokens)
     for segs in prepared.attached.values():
         for job, _ in segs:
-            seen[job.requests[0]].extend(job.tokens)
+            for r in job.requests:
+                seen[r].extend(job.tokens)
     return all(sorted(seen[r]) == sorted(path) for r, path in enumerate(tree.paths))
 
 
@@ -283,7 +284,8 @@ def test_nodes_of_a_wave_attach():
     for native in (True, False):
         if native and not _planner.available():
             continue
-        p = prepare(plan, q) if native else _prepare_python_attach(plan, q)
+        # consolidate_rows=0: the 20-row gapped job would otherwise take the root into 64-row items
+        p = prepare(plan, q, consolidate_rows=0) if native else _prepare_python_attach(plan, q, consolidate_rows=0)
         segs = [(job.requests, lrow) for s in p.attached.values() for job, lrow in s]
         for b in range(4):
             assert (tuple(range(8 * b, 8 * b + 8)), 32 * b) in segs
@@ -298,12 +300,12 @@ def test_nodes_of_a_wave_attach():
         assert _covers_paths_plan(p, plan, 32)
 
 
-def _prepare_python_attach(plan, q):
+def _prepare_python_attach(plan, q, **kw):
     """prepare() with the Python attachment (kernels._attach_tails_py) instead of the host library's."""
     orig = kernels._attach_tails
     kernels._attach_tails = kernels._attach_tails_py
     try:
-        return prepare(plan, q)
+        return prepare(plan, q, **kw)
     finally:
         kernels._attach_tails = orig
 
@@ -373,7 +375,45 @@ def test_jobs_over_one_token_run_fuse():
     assert sorted(j.requests for j in fused.jobs) == [tuple(range(40))] * 2
     apart = prepare(Plan([a, b, c], "x", 0.0, settings), q, fuse_rows=161)
     assert sorted(len(j.requests) for j in apart.jobs) == [20, 20, 40]
+    # per-request jobs (4 rows each) over one token run stay apart, whatever their number
+    single = [Job((r,), tuple(range(0, 64))) for r in range(40)]
+    alone = prepare(Plan(single + [c], "x", 0.0, settings), q, fuse_rows=1)
+    assert sorted(j.requests for j in alone.jobs if j.tokens[0] < 64) == [(r,) for r in range(40)]
     shared = Job(tuple(range(19, 39)), tuple(range(0, 64)))   # request 19 in both
     q2 = torch.empty(39, 4, 32, dtype=torch.float16)
     kept = prepare(Plan([a, shared, Job((39 - 1,), (200,))], "x", 0.0, settings), q2, fuse_rows=1)
     assert sorted(len(j.requests) for j in kept.jobs if j.tokens[0] == 0) == [20, 20]
+
+
+def test_wide_jobs_consolidate_into_64_row_items():
+    """When 64-row items run anyway and no wider job holds more than consolidate_rows rows,
+    the wider jobs run as 16-request (64-row) groups in the same kind: the layer launches one
+    large-job kernel.  A group of at most 16 rows becomes a small job.  A wider job above the
+    limit keeps the 256-row kind."""
+    settings = dict(kvheads=2)
+    q = torch.empty(40, 8, 32, dtype=torch.float16)   # group 4
+    root = Job(tuple(range(35)), tuple(range(0, 640)))             # 140 rows
+    half = Job(tuple(range(16)), tuple(range(640, 1280)))          # 64 rows: a 64-row item
+    tails = [Job((r,), tuple(range(1280 + 40 * r, 1320 + 40 * r))) for r in range(40)]
+    others = [Job(tuple(range(35, 40)), tuple(range(0, 640)))]     # the rest of the root's requests
+    plan = Plan([root, half] + others + tails, "x", 0.0, settings)
+    nreq = 40
+    wide = prepare(plan, q, consolidate_rows=128, route_items=0)   # 140 rows > 128: kept
+    assert wide.abi.n_items[_native.TA_LARGE256] > 0
+    one = prepare(plan, q, consolidate_rows=160, route_items=0)
+    assert one.abi.n_items[_native.TA_LARGE256] == 0 and one.abi.n_items[_native.TA_LARGE64] > 0
+    groups = {j.requests for j in one.jobs if j.tokens[0] < 640}
+    assert {tuple(range(0, 16)), tuple(range(16, 32))} <= groups and (32, 33, 34) in groups
+    small = {j.requests for j in one.jobs[:one.small_jobs]}
+    assert (32, 33, 34) in small                                   # 12 rows: a small job
+    for p in (wide, one, prepare(plan, q, consolidate_rows=0, route_items=0), prepare(plan, q)):
+        assert _covers_paths_plan(p, plan, nreq)
+    # the 81-shape grid's 32-request, 99 %-shared, 3-level tree under the fitted model
+    spec = next(s for p_, s in shapes.config_grid()
+                if p_ == {"requests": 32, "context": 8192, "fraction": 0.99, "depth": 3})
+    tree = shapes.tree(spec)
+    q = torch.empty(32, 32, 128, dtype=torch.bfloat16)
+    fitted = schedule(tree, 32, 8, 128, "cube", CostModel.mi355x())
+    p = prepare(fitted, q)
+    assert p.abi.n_items[_native.TA_LARGE256] == 0 and _covers_paths(p, tree)
+    assert prepare(fitted, q, consolidate_rows=0).abi.n_items[_native.TA_LARGE256] > 0

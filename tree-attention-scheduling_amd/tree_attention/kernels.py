@@ -187,6 +187,9 @@ ATTACH_MIN_CAP = 2 * XTAIL_MAX
 ROUTE_ITEMS = 768
 # jobs over one token run execute as one job when together they fill a 256-row work item
 FUSE_ROWS = 256
+# wider large jobs run as 64-row request groups when 64-row items run anyway and no wider
+# job exceeds this many rows (prepare's consolidate_rows; 0: never)
+CONSOLIDATE_ROWS = 128
 
 
 def _tiles(job) -> int:
@@ -297,17 +300,20 @@ def _attach_tails_py(small, large, group, tile_rows, is_fixed, min_cap=ATTACH_MI
 
 
 def _fuse_same_tokens(jobs, group, min_rows):
-    """Jobs over the same token run run as one job over the union of their requests when
-    together they hold at least ``min_rows`` query rows and share no request.
+    """Large jobs (more than 16 query rows) over the same token run run as one job over the
+    union of their requests when together they hold at least ``min_rows`` query rows and
+    share no request.
 
     Each request keeps one partial over those tokens, so the attention is the same; the K/V
     run is streamed once per 256-row work item instead of once per job.  A plan that splits
     a wide node into request groups (a cost model with 64-row query tiles) then runs the node
-    in the 256-row kernel.  The fused job takes the place of the first of its jobs.
+    in the 256-row kernel.  Jobs of a few requests -- the per-request plan's among them --
+    are left as planned.  The fused job takes the place of the first of its jobs.
     """
     runs = {}
     for j in jobs:
-        runs.setdefault((j.tokens[0], len(j.tokens)), []).append(j)
+        if len(j.requests) * group > SMALL_ROWS:
+            runs.setdefault((j.tokens[0], len(j.tokens)), []).append(j)
     fused = {}
     for key, grp in runs.items():
         if len(grp) < 2:
@@ -320,7 +326,7 @@ def _fuse_same_tokens(jobs, group, min_rows):
     out = []
     for j in jobs:
         key = (j.tokens[0], len(j.tokens))
-        if key not in fused:
+        if key not in fused or len(j.requests) * group <= SMALL_ROWS:
             out.append(j)
         elif fused[key] is not None:
             out.append(fused[key])
@@ -513,15 +519,16 @@ def _metadata_numpy(jobs, small_jobs, nreq, group, kvheads, tile_rows, attached,
 
 
 def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int | None = None,
-            attach_tails: bool = True, route_items: int = ROUTE_ITEMS, fuse_rows: int = FUSE_ROWS) -> PreparedPlan:
+            attach_tails: bool = True, route_items: int = ROUTE_ITEMS, fuse_rows: int = FUSE_ROWS,
+            consolidate_rows: int = CONSOLIDATE_ROWS) -> PreparedPlan:
     """Lower ``plan`` to device metadata and scratch for queries shaped like ``q``.
 
     Mirrors kernels.py:103-141: physical jobs, stable small-first order, one
     host-to-device copy of all int32 metadata, scratch allocated once.
     ``tile_rows`` (64, 128 or 256) caps the query rows one workgroup of the
     large-job kernels handles; it changes the work split, not the result.
-    Jobs over the same token run that together hold at least ``fuse_rows`` query
-    rows (0: never) run as one (``_fuse_same_tokens``).  Runs of jobs over one request group are re-cut for the
+    Large jobs over the same token run that together hold at least ``fuse_rows``
+    query rows (0: never) run as one (``_fuse_same_tokens``).  Runs of jobs over one request group are re-cut for the
     GPU (``_recut``), so ``jobs`` holds the execution jobs; ``fixed_from`` keeps jobs whose tokens
     start at or after it (decode tails whose length changes) as they are.
     ``attach_tails`` folds private single-request jobs into the 256-row work
@@ -562,24 +569,46 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     def growing(job):
         return fixed_from is not None and job.tokens[0] >= fixed_from
 
-    large = _recut(large, lambda r: -(-len(r) * group // _native.KIND_ROWS[_large_kind(len(r) * group, tile_rows)])
-                   * kvheads, n_cu, growing)
-    # chunks of one token range side by side: a root split into request groups then gives
-    # request r its k-th slot at r + k * (requests of a chunk), the layout the merge computes
-    large.sort(key=lambda j: (j.tokens[0], j.requests[0]))
-    attached = {}
-    if attach_tails:  # growing tails too: their records' token fields are rewritten by fill_growing
-        # candidates: the small jobs, then the large ones whose rows fit one wave
-        mids = [j for j in large if len(j.requests) * group <= WAVE_ROWS]
-        left, attached = _attach_tails(small + mids, large, group, tile_rows, lambda job: False)
-        if any(len(j.requests) * group <= SMALL_ROWS for j in left):
-            # the small-job kernel launches anyway: items take no more attached tiles than
-            # their own, so that the large kernel does not become the longer of the two
-            left, attached = _attach_tails(small + mids, large, group, tile_rows, lambda job: False, 0)
-        small = [j for j in left if len(j.requests) * group <= SMALL_ROWS]
-        if mids:
-            gone = {id(job) for segs in attached.values() for job, _ in segs}
-            large = [j for j in large if id(j) not in gone]
+    def lower(small, large):
+        """Re-cut, order and attach: (small jobs, large jobs, attachments)."""
+        large = _recut(large, lambda r: -(-len(r) * group // _native.KIND_ROWS[_large_kind(len(r) * group, tile_rows)])
+                       * kvheads, n_cu, growing)
+        # chunks of one token range side by side: a root split into request groups then gives
+        # request r its k-th slot at r + k * (requests of a chunk), the layout the merge computes
+        large.sort(key=lambda j: (j.tokens[0], j.requests[0]))
+        attached = {}
+        if attach_tails:  # growing tails too: their records' token fields are rewritten by fill_growing
+            # candidates: the small jobs, then the large ones whose rows fit one wave
+            mids = [j for j in large if len(j.requests) * group <= WAVE_ROWS]
+            left, attached = _attach_tails(small + mids, large, group, tile_rows, lambda job: False)
+            if any(len(j.requests) * group <= SMALL_ROWS for j in left):
+                # the small-job kernel launches anyway: items take no more attached tiles than
+                # their own, so that the large kernel does not become the longer of the two
+                left, attached = _attach_tails(small + mids, large, group, tile_rows, lambda job: False, 0)
+            small = [j for j in left if len(j.requests) * group <= SMALL_ROWS]
+            if mids:
+                gone = {id(job) for segs in attached.values() for job, _ in segs}
+                large = [j for j in large if id(j) not in gone]
+        return small, large, attached
+
+    large0 = large
+    small, large, attached = lower(small0, large0)
+    # One large-job kind: when 64-row items run anyway and every wider job holds at most
+    # consolidate_rows rows, the wider jobs run as 64-row request groups in the same kind
+    # (one launch and its start-up less; their K/V is read once per group).
+    per64 = 64 // group
+    wide = [j for j in large0 if len(j.requests) * group > 64]
+    if (consolidate_rows and per64 and wide and all(len(j.requests) * group <= consolidate_rows for j in wide)
+            and any(_large_kind(len(j.requests) * group, tile_rows) == _native.TA_LARGE64 for j in large)):
+        split = []
+        for j in large0:
+            if len(j.requests) * group > 64:
+                split += [Job(j.requests[i:i + per64], j.tokens) for i in range(0, len(j.requests), per64)]
+            else:
+                split.append(j)
+        # a last group of at most 16 rows is a small job
+        small, large, attached = lower(small0 + [j for j in split if len(j.requests) * group <= SMALL_ROWS],
+                                       [j for j in split if len(j.requests) * group > SMALL_ROWS])
     if small and routed and sum(map(_tiles, routed)) * kvheads <= route_items:
         small, large, attached = small0 + routed, [], {}
     # Tails (a request's only small job) stay whole when they alone fill the GPU,
@@ -648,7 +677,8 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     return PreparedPlan(jobs, small_jobs, True, contiguous_q, qids_t, kids_t, qlen_t, klen_t,
                         slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t,
                         keyed, xtail_t if attached else None, plan,
-                        {"tile_rows": tile_rows, "fixed_from": fixed_from, "route_items": route_items, "fuse_rows": fuse_rows}, None,
+                        {"tile_rows": tile_rows, "fixed_from": fixed_from, "route_items": route_items, "fuse_rows": fuse_rows,
+                         "consolidate_rows": consolidate_rows}, None,
                         meta["qbase"].tolist(),
                         grow_offsets=grow_offsets)
 
