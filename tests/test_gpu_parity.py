@@ -515,6 +515,45 @@ def test_graph_replay_matches_eager(device):
         assert not torch.equal(other, eager)
 
 
+@pytest.mark.parametrize("d,dtype", [(128, torch.bfloat16), (64, torch.float16), (32, torch.bfloat16)])
+def test_mixed_kinds_launch_equals_kind_by_kind(d, dtype, device):
+    """A layer with 256-row, 64-row and small work items runs them in one launch
+    (seg_mix_kernel): the output has the bits of the kinds launched one after another
+    (ta_segment_plan per kind, then the merge) and matches the oracle."""
+    n = 96
+    jobs = [Job(tuple(range(64)), tuple(range(0, 300))),            # 256 rows: TA_LARGE256
+            Job(tuple(range(64, 80)), tuple(range(300, 500)))]      # 64 rows: TA_LARGE64
+    # two private runs per request (apart, so that neither is a merging tail): small jobs
+    jobs += [Job((r,), tuple(range(500 + 60 * r + o, 525 + 60 * r + o))) for r in range(80) for o in (0, 30)]
+    jobs += [Job((r,), tuple(range(5300 + 20 * (r - 80), 5320 + 20 * (r - 80)))) for r in range(80, n)]
+    jobs += [Job((r,), tuple(range(5700 + 20 * (r - 80), 5710 + 20 * (r - 80)))) for r in range(80, n)]
+    paths = [[] for _ in range(n)]
+    for job in jobs:
+        for r in job.requests:
+            paths[r].extend(job.tokens)
+    tree = _Paths([tuple(p) for p in paths])
+    g = torch.Generator().manual_seed(d)
+    q = torch.randn(n, 32, d, generator=g).to(dtype)
+    k = torch.randn(6024, 8, d, generator=g).to(dtype)
+    v = torch.randn(6024, 8, d, generator=g).to(dtype)
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    # no routing and no attachment: every kind keeps its items (the grid and nested-tree
+    # tests run the mixed launch with attached segments)
+    prepared = prepare(Plan(jobs, "x", 0.0, dict(kvheads=8)), qd, route_items=0, attach_tails=False)
+    kinds = [kd for kd in (_native.TA_LARGE256, _native.TA_LARGE64, _native.TA_SMALL) if prepared.abi.n_items[kd] > 0]
+    say("mixed kinds", d, dtype, list(prepared.abi.n_items))
+    assert len(kinds) == 3 and prepared.abi.n_items[_native.TA_TAIL] == 0 and prepared.abi.n_items[_native.TA_LARGE128] == 0
+    a = attention_matrix(qd, kp, vp, prepared).clone()
+    prepared.out.zero_()
+    for kd in kinds:
+        segment(qd, kp, vp, prepared, kd)
+    b = merge(prepared, kp).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    check(a, oracle_fp32(q, k, v, tree), 0.008, 0.03, f"mixed/{d}")
+
+
 def _rotate_half(x):
     half = x.shape[-1] // 2
     return torch.cat((-x[..., half:], x[..., :half]), dim=-1)

@@ -310,30 +310,43 @@ struct TileMath {
     }
 };
 
-template <int D, bool FP16, int NB, int NW, int STAGES>
-__global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
+// Work item of linear block b of n: block b runs on XCD b % 8, and every XCD
+// gets a contiguous range of items, so that row tiles of one (job, head)
+// share its L2.
+__device__ inline int xcd_item(int b, int n) {
+    const int xcd = b & 7, slot = b >> 3;
+    const int q8 = n >> 3, rm = n & 7;
+    return xcd * q8 + min(xcd, rm) + slot;
+}
+
+// The waves of a work item meet at a barrier, unless one wave works alone on
+// its own LDS stage (SOLO), where its own vmcnt wait orders copy and reads.
+template <bool SOLO>
+__device__ inline void item_barrier() {
+    if constexpr (!SOLO) __builtin_amdgcn_s_barrier();
+}
+
+// One work item (job, first row, KV head) of the tile kernels: NW waves, NB
+// 16-row blocks per wave, STAGES LDS stages at `lds`.  The item holds rows
+// [row0, row0 + item_rows) of its job.  SOLO: one wave alone (tid = its lane).
+template <int D, bool FP16, int NB, int NW, int STAGES, bool SOLO = false>
+__device__ __forceinline__ void tile_item(const SegParams &p, const int32_t *__restrict__ items, int item,
+                                          u16 *lds, int tid, int item_rows) {
     using T = Tile<D>;
     using M = TileMath<D, FP16, NB, NW>;
     constexpr int KS = M::KS;
     constexpr int BPW = T::NBLK / NW;  // copies per wave per tile
     static_assert(T::NBLK % NW == 0, "every wave copies the same number of blocks");
     static_assert(STAGES >= 1 && STAGES <= 3, "one to three LDS stages");
-    __shared__ __attribute__((aligned(16))) u16 lds[STAGES * T::ELEMS];
+    static_assert(!SOLO || (NW == 1 && STAGES == 1), "a wave alone has one stage");
+    const int job = items[3 * item], row0 = items[3 * item + 1], h = items[3 * item + 2];
 
-    // Linear block L runs on XCD L % 8; give every XCD a contiguous range of
-    // items so that row tiles of one (job, head) share an L2.
-    const int total = gridDim.x;
-    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-    const int q8 = total >> 3, rm = total & 7;
-    const int item = xcd * q8 + min(xcd, rm) + slot;
-    const int job = p.items[3 * item], row0 = p.items[3 * item + 1], h = p.items[3 * item + 2];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = SOLO ? 0 : tid >> 6;
     const int row = lane & 15, g4 = lane >> 4;
     const int kst = p.kstart[job];
     const int ntok = max(0, min(p.klen[job], p.tcap - kst));
     const int kend = kst + ntok;
-    const int nrows = p.qlen[job] * p.group;
+    const int nrows = min(p.qlen[job] * p.group, row0 + item_rows);
     const int wrow0 = row0 + 16 * NB * wave;
     const bool active = wrow0 < nrows;
 
@@ -371,10 +384,10 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
         // one stage (one-wave workgroups, four per CU): copy, wait, compute
         for (int it = 0; it < ntiles; ++it) {
             const int t0 = tb0 + it * T::TT;
-            if (it > 0) __builtin_amdgcn_s_barrier();  // every wave is done with the previous tile
+            if (it > 0) item_barrier<SOLO>();  // every wave is done with the previous tile
             acc.copy(lds, p.kp, p.vp, h, p.tcap, t0, kst, kend, wave, lane);
             __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
-            __builtin_amdgcn_s_barrier();
+            item_barrier<SOLO>();
             if (active) acc.tile(lds, qf, of, max(0, kst - t0), min(T::TT, kend - t0), g4, p.scale_log2);
         }
     } else {
@@ -391,7 +404,7 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
                 __builtin_amdgcn_s_waitcnt(TA_VMCNT(BPW));
             else
                 __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
-            __builtin_amdgcn_s_barrier();  // every copy of tile it landed; stage of tile it-1 is free
+            item_barrier<SOLO>();  // every copy of tile it landed; stage of tile it-1 is free
         }
         const int ns = cs == 0 ? STAGES - 1 : cs - 1;  // stage of tile it+AHEAD (that of tile it-1)
         const int t0 = tb0 + it * T::TT;
@@ -412,6 +425,12 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
         const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
         store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4);
     }
+}
+
+template <int D, bool FP16, int NB, int NW, int STAGES>
+__global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
+    __shared__ __attribute__((aligned(16))) u16 lds[STAGES * Tile<D>::ELEMS];
+    tile_item<D, FP16, NB, NW, STAGES>(p, p.items, xcd_item(blockIdx.x, gridDim.x), lds, threadIdx.x, 16 * NB * NW);
 }
 
 // ------------------------------------------------------------------------
@@ -592,8 +611,11 @@ struct PipeMath {
 // (the pipelined steps read one step ahead), so SYNC+1 tiles are resident
 // and STAGES-SYNC-1 more can be in flight.  The prologue issues PRO tiles;
 // the first loop barrier issues the rest of the ring.
+// One 256-row work item of the pipelined kernel, with its attached segments
+// (p.xtail, indexed by the item), STAGES LDS stages at `lds`.
 template <int D, bool FP16, int NW, int NB = 2, int STAGES = TA_PIPE_STAGES, int SYNC = 1, int PRO = TA_PIPE_PRO>
-__global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
+__device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__restrict__ items, int item, u16 *lds,
+                                          int tid) {
     using T = Tile<D>;
     using M = PipeMath<D, FP16, NW, NB>;
     using TM = TileMath<D, FP16, NB, NW>;
@@ -603,15 +625,9 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     static_assert(SYNC >= 1 && STAGES >= 2 * SYNC + 1 && STAGES <= 5,
                   "a group's tiles, the next K and the next group's copies fit the stages");
     static_assert(PRO >= SYNC + 1 && PRO <= STAGES, "the prologue issues the tiles the first group reads");
-    __shared__ __attribute__((aligned(16))) u16 lds[STAGES * T::ELEMS];
+    const int job = items[3 * item], row0 = items[3 * item + 1], h = items[3 * item + 2];
 
-    const int total = gridDim.x;
-    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-    const int q8 = total >> 3, rm = total & 7;
-    const int item = xcd * q8 + min(xcd, rm) + slot;
-    const int job = p.items[3 * item], row0 = p.items[3 * item + 1], h = p.items[3 * item + 2];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = tid >> 6;
     const int row = lane & 15, g4 = lane >> 4;
     const int kst = p.kstart[job];
     const int ntok = max(0, min(p.klen[job], p.tcap - kst));
@@ -802,6 +818,40 @@ __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     }
 }
 
+template <int D, bool FP16, int NW>
+__global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
+    __shared__ __attribute__((aligned(16))) u16 lds[TA_PIPE_STAGES * Tile<D>::ELEMS];
+    pipe_item<D, FP16, NW>(p, p.items, xcd_item(blockIdx.x, gridDim.x), lds, threadIdx.x);
+}
+
+// Work items of several kinds of one layer in one launch of 512-thread
+// workgroups: blocks [0, base[1]) run 256-row items (with their attached
+// segments), blocks [base[1], base[2]) run 64-row items on eight waves (the
+// upper four copy and meet at the barriers), and the blocks from base[2] on
+// run four small items each, one per wave on its own stage (the upper four
+// waves end at once).  The bases are multiples of 8, so that every kind's
+// items map to XCDs as in its own kernel; blocks past a kind's item count end
+// at once.  The kinds run side by side instead of one launch after another.
+template <int D, bool FP16>
+__global__ __launch_bounds__(512) void seg_mix_kernel(MixParams mp) {
+    using T = Tile<D>;
+    __shared__ __attribute__((aligned(16))) u16 lds[TA_PIPE_STAGES * T::ELEMS];
+    static_assert(TA_PIPE_STAGES >= 4 && 3 <= TA_PIPE_STAGES, "four small stages and three 64-row stages fit");
+    const int b = blockIdx.x, tid = threadIdx.x;
+    if (b < mp.base[1]) {
+        if (b >= mp.n[0]) return;
+        pipe_item<D, FP16, 8>(mp.p, mp.items[0], xcd_item(b, mp.n[0]), lds, tid);
+    } else if (b < mp.base[2]) {
+        const int lb = b - mp.base[1];
+        if (lb >= mp.n[1]) return;
+        tile_item<D, FP16, 1, 8, 3>(mp.p, mp.items[1], xcd_item(lb, mp.n[1]), lds, tid, 64);
+    } else {
+        const int wave = tid >> 6, it = 4 * (b - mp.base[2]) + wave;
+        if (wave >= 4 || it >= mp.n[2]) return;
+        tile_item<D, FP16, 1, 1, 1, true>(mp.p, mp.items[2], it, lds + wave * T::ELEMS, tid & 63, 16);
+    }
+}
+
 // ------------------------------------------------------------------------
 // Tail kernel with the merge fused in (TA_TAIL items with out given).  One
 // two-wave workgroup per (tail job, KV head): the job's single request has
@@ -982,7 +1032,36 @@ hipError_t launch_d(const SegParams &sp, int kind, hipStream_t stream) {
     return hipGetLastError();
 }
 
+template <int D, bool FP16>
+hipError_t launch_mix_d(const MixParams &mp, int blocks, hipStream_t stream) {
+    TA_LAUNCH((seg_mix_kernel<D, FP16>), dim3(blocks), dim3(512), stream, mp);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_tile_mix(const SegParams &sp, const int32_t *const items[3], const int n[3], int d, bool fp16,
+                           hipStream_t stream) {
+    if (sp.tcap % 8 != 0) return hipErrorNotSupported;
+    MixParams mp;
+    mp.p = sp;
+    int base = 0;
+    for (int k = 0; k < 3; ++k) {
+        mp.items[k] = items[k];
+        mp.n[k] = n[k] > 0 ? n[k] : 0;
+        mp.base[k] = base;
+        const int blocks = k < 2 ? mp.n[k] : (mp.n[k] + 3) / 4;
+        base += (blocks + 7) & ~7;
+    }
+    const int blocks = mp.base[2] + (mp.n[2] + 3) / 4;
+    if (blocks <= 0) return hipSuccess;
+    switch (d) {
+        case 128: return fp16 ? launch_mix_d<128, true>(mp, blocks, stream) : launch_mix_d<128, false>(mp, blocks, stream);
+        case 64: return fp16 ? launch_mix_d<64, true>(mp, blocks, stream) : launch_mix_d<64, false>(mp, blocks, stream);
+        case 32: return fp16 ? launch_mix_d<32, true>(mp, blocks, stream) : launch_mix_d<32, false>(mp, blocks, stream);
+        default: return hipErrorNotSupported;
+    }
+}
 
 hipError_t launch_tile(const SegParams &sp, int kind, int d, bool fp16, hipStream_t stream) {
     if (sp.tcap % 8 != 0) return hipErrorNotSupported;

@@ -173,8 +173,25 @@ extern thread_local LaunchEvents g_launch_events;
         }                                                                                             \
     } while (0)
 
+// Work items of several kinds in one launch (segment_tile.hip's
+// seg_mix_kernel): p's fields but items / n_items, then per kind --
+// TA_LARGE256 (with p.xtail), TA_LARGE64, TA_SMALL -- the item array, its
+// count and the first block of the kind (a multiple of 8).
+struct MixParams {
+    SegParams p;
+    const int32_t *items[3];
+    int n[3];
+    int base[3];
+};
+
 // Large-job launcher of segment_tile.hip (gfx950 LDS-transpose kernels).
 // Returns hipErrorNotSupported when the shape is outside what it handles.
 hipError_t launch_tile(const SegParams &sp, int kind, int d, bool fp16, hipStream_t stream);
+
+// One launch of the TA_LARGE256, TA_LARGE64 and TA_SMALL items items[k]
+// (n[k] of each) of one layer, side by side (hipErrorNotSupported unless the
+// pool capacity is a multiple of 8).
+hipError_t launch_tile_mix(const SegParams &sp, const int32_t *const items[3], const int n[3], int d, bool fp16,
+                           hipStream_t stream);
 
 }  // namespace ta

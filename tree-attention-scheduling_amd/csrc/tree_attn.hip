@@ -618,6 +618,12 @@ const char *ta_error_string(int code) {
 
 namespace {
 
+void fill_params(SegParams &sp, const void *q, const void *kp, const void *vp, const int32_t *qids,
+                 const int32_t *kstart, const int32_t *qlen, const int32_t *klen, const int32_t *rowbase,
+                 const int32_t *items, int32_t n_items, void *part, float *lse, int32_t hq, int32_t hk, int32_t d,
+                 int32_t tcap, int32_t maxr, const int32_t *slots, const int32_t *counts, void *out, int32_t maxs,
+                 const int32_t *xtail, int32_t xtail_stride, const int32_t *qbase);
+
 // One segment launch; with out given (TA_TAIL only) the items merge their
 // requests into out.
 int segment_launch(const void *q, const void *kp, const void *vp, const int32_t *qids, const int32_t *kstart,
@@ -646,6 +652,20 @@ int segment_launch(const void *q, const void *kp, const void *vp, const int32_t 
         if (kind != TA_LARGE256 || tcap % 8 != 0 || xtail_stride != TA_XTAIL_STRIDE) return TA_ERR_ARG;
     }
     SegParams sp;
+    fill_params(sp, q, kp, vp, qids, kstart, qlen, klen, rowbase, items, n_items, part, lse, hq, hk, d, tcap, maxr,
+                slots, counts, out, maxs, xtail, xtail_stride, qbase);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+#define TA_SEG(D, F) launch_segment<D, F>(sp, kind, st)
+    return (int)TA_DISPATCH(d, dtype == TA_FP16, TA_SEG);
+#undef TA_SEG
+}
+
+// The launch arguments every segment kernel shares.
+void fill_params(SegParams &sp, const void *q, const void *kp, const void *vp, const int32_t *qids,
+                 const int32_t *kstart, const int32_t *qlen, const int32_t *klen, const int32_t *rowbase,
+                 const int32_t *items, int32_t n_items, void *part, float *lse, int32_t hq, int32_t hk, int32_t d,
+                 int32_t tcap, int32_t maxr, const int32_t *slots, const int32_t *counts, void *out, int32_t maxs,
+                 const int32_t *xtail, int32_t xtail_stride, const int32_t *qbase) {
     sp.q = static_cast<const u16 *>(q);
     sp.kp = static_cast<const u16 *>(kp);
     sp.vp = static_cast<const u16 *>(vp);
@@ -671,10 +691,6 @@ int segment_launch(const void *q, const void *kp, const void *vp, const int32_t 
     sp.xtail = xtail;
     sp.xtail_stride = xtail_stride;
     sp.qbase = qbase;
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-#define TA_SEG(D, F) launch_segment<D, F>(sp, kind, st)
-    return (int)TA_DISPATCH(d, dtype == TA_FP16, TA_SEG);
-#undef TA_SEG
 }
 
 int plan_segment(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan, int kind,
@@ -757,6 +773,37 @@ static __device__ __align__(256) unsigned char scratch[TA_NOALLOC_SCRATCH_BYTES]
 
 namespace {
 
+// The TA_LARGE256, TA_LARGE64 and TA_SMALL items of a plan in one launch
+// (seg_mix_kernel), when at least two of those kinds have items and
+// TA_LARGE128 has none.  Returns -1 when the plan does not qualify.
+int mix_launch(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan, void *stream) {
+#ifdef TA_LEGACY_LARGE
+    return -1;
+#endif
+    const int n[3] = {plan->n_items[TA_LARGE256], plan->n_items[TA_LARGE64], plan->n_items[TA_SMALL]};
+    if ((n[0] > 0) + (n[1] > 0) + (n[2] > 0) < 2 || plan->n_items[TA_LARGE128] > 0 || tcap % 8 != 0) return -1;
+    if (n[0] < 0 || n[1] < 0 || n[2] < 0) return TA_ERR_ARG;
+    if (int e = check_common(plan->hq, plan->hk, plan->d, plan->dtype)) return e;
+    if (plan->nreq <= 0 || tcap <= 0 || plan->maxr <= 0) return TA_ERR_ARG;
+    if (!q || !kp || !vp || !plan->qids || !plan->kstart || !plan->qlen || !plan->klen || !plan->rowbase ||
+        !plan->part || !plan->lse)
+        return TA_ERR_ARG;
+    for (int k : {TA_LARGE256, TA_LARGE64, TA_SMALL})
+        if (plan->n_items[k] > 0 && !plan->items[k]) return TA_ERR_ARG;
+    if (!aligned16(q) || !aligned16(kp) || !aligned16(vp) || !aligned16(plan->part)) return TA_ERR_ALIGN;
+    const bool xt = n[0] > 0 && plan->xtail;
+    if (xt && plan->xtail_stride != TA_XTAIL_STRIDE) return TA_ERR_ARG;
+    SegParams sp;
+    fill_params(sp, q, kp, vp, plan->qids, plan->kstart, plan->qlen, plan->klen, plan->rowbase, nullptr, 0,
+                plan->part, plan->lse, plan->hq, plan->hk, plan->d, tcap, plan->maxr, plan->slots, plan->counts,
+                nullptr, plan->maxs, xt ? plan->xtail : nullptr, xt ? plan->xtail_stride : 0, plan->qbase);
+    const int32_t *const items[3] = {plan->items[TA_LARGE256], plan->items[TA_LARGE64], plan->items[TA_SMALL]};
+    if (hipError_t e = ta::launch_tile_mix(sp, items, n, plan->d, plan->dtype == TA_FP16,
+                                           static_cast<hipStream_t>(stream)))
+        return (int)e;
+    return 0;
+}
+
 int attention_layer(const void *q, const void *kp, const void *vp, int32_t tcap, const ta_plan *plan, void *out,
                     void *stream) {
     if (!plan || !out) return TA_ERR_ARG;
@@ -767,9 +814,13 @@ int attention_layer(const void *q, const void *kp, const void *vp, int32_t tcap,
 #endif
     // attached segments exist only on the LDS-transpose path (pools with tcap % 8 == 0)
     if (plan->xtail && !fused) return TA_ERR_ARG;
-    // the partials every merge reads come first: large jobs, then small jobs
+    // the partials every merge reads come first: large jobs, then small jobs,
+    // in one launch when the kinds allow it
+    const int mixed = mix_launch(q, kp, vp, tcap, plan, stream);
+    if (mixed > 0) return mixed;
     static const int order[] = {TA_LARGE256, TA_LARGE128, TA_LARGE64, TA_SMALL};
     for (int kind : order) {
+        if (mixed == 0 && kind != TA_LARGE128) continue;
         if (plan->n_items[kind] == 0) continue;
         if (int e = plan_segment(q, kp, vp, tcap, plan, kind, nullptr, stream)) return e;
     }
