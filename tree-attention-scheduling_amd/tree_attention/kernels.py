@@ -187,6 +187,12 @@ ATTACH_MIN_CAP = 2 * XTAIL_MAX
 ROUTE_ITEMS = 768
 # jobs over one token run execute as one job when together they fill a 256-row work item
 FUSE_ROWS = 256
+# tails (a request's only small job) stay whole, one merging work item each, when they fill
+# the GPU; tails longer than one tile only with four items per CU, since each item streams
+# its tail alone (measured on the six benchmark cases and the 81-shape grid: 0.92x over
+# the 13 layers it changes, 0.78x at best)
+TAIL_KEEP_TILES = 1
+TAIL_KEEP_ITEMS_PER_CU = 4
 # wider large jobs run as 64-row request groups when 64-row items run anyway and no wider
 # job exceeds this many rows (prepare's consolidate_rows; 0: never)
 CONSOLIDATE_ROWS = 128
@@ -618,7 +624,11 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
         for r in j.requests:
             owners[r] = owners.get(r, 0) + 1
     tails = [j for j in small if len(j.requests) == 1 and owners[j.requests[0]] == 1]
-    keep = {id(j) for j in tails} if len(tails) * kvheads >= n_cu else set()
+    # (a work item streams its tail alone: tails longer than TAIL_KEEP_TILES tiles are re-cut
+    # unless there are enough of them for TAIL_KEEP_ITEMS_PER_CU items per CU)
+    longest = max((_tiles(j) for j in tails), default=0)
+    enough = len(tails) * kvheads >= n_cu * (1 if longest <= TAIL_KEEP_TILES else TAIL_KEEP_ITEMS_PER_CU)
+    keep = {id(j) for j in tails} if enough else set()
     small = _recut(small, lambda r: kvheads, 8 * n_cu, lambda j: growing(j) or id(j) in keep)
     jobs = small + large
     small_jobs = len(small)
