@@ -417,3 +417,41 @@ def test_wide_jobs_consolidate_into_64_row_items():
     p = prepare(fitted, q)
     assert p.abi.n_items[_native.TA_LARGE256] == 0 and _covers_paths(p, tree)
     assert prepare(fitted, q, consolidate_rows=0).abi.n_items[_native.TA_LARGE256] > 0
+
+
+def test_one_tile_chunks_lengthen_when_the_lowering_keeps_its_kinds():
+    """The re-cut gives large chunks of at least LARGE_MIN_TILES tiles when the lowering
+    then keeps its kernel kinds, attaches as much and still has half a work item per CU."""
+    assert kernels.LARGE_MIN_TILES == 2
+    # "wide": 32 requests over 2048 shared tokens + 64 private each, fitted model.  One
+    # tile per chunk gives 32 chunks x 8 heads = 256 items; two tiles give 128 items
+    tree = shapes.tree(shapes.benchmark_cases()["wide"])
+    q = torch.empty(32, 32, 128, dtype=torch.bfloat16)
+    plan = schedule(tree, 32, 8, 128, "cube", CostModel.mi355x())
+    one = prepare(plan, q, large_min_tiles=1)
+    two = prepare(plan, q)
+    assert one.abi.n_items[_native.TA_LARGE256] == 256 and two.abi.n_items[_native.TA_LARGE256] == 128
+    assert {len(j.tokens) for j in one.jobs} == {64} and {len(j.tokens) for j in two.jobs} == {128}
+    # every private tail attached in both: no small-job launch
+    assert one.small_jobs == two.small_jobs == 0
+    assert sum(map(len, one.attached.values())) == sum(map(len, two.attached.values())) == 32
+    assert two.abi.nslot * 2 == one.abi.nslot
+    assert _covers_paths(one, tree) and _covers_paths(two, tree)
+    # chunks of at least two tiles already (the headline root): nothing changes
+    head = shapes.tree(shapes.headline())
+    qh = torch.empty(128, 32, 128, dtype=torch.bfloat16)
+    hp = schedule(head, 32, 8, 128, "cube", CostModel.mi355x())
+    a, b = prepare(hp, qh, large_min_tiles=1), prepare(hp, qh)
+    assert [(j.requests, j.tokens) for j in a.jobs] == [(j.requests, j.tokens) for j in b.jobs]
+    # the Qwen3-4B-shaped decode layer: two-tile chunks would leave its tails and branch
+    # nodes unattached, so the lowering stays as it is
+    qt = KVTree.from_sequences(shapes.qwen3_4b_workload())
+    qq = torch.empty(len(qt.paths), 32, 128, dtype=torch.bfloat16)
+    qp = schedule(qt, 32, 8, 128, "cube", CostModel.mi355x())
+    t0 = qt.storage_tokens   # 16 reserved tokens per request, as CachedDecodePlan lays them out
+    tails = [Job((r,), tuple(range(t0 + 16 * r, t0 + 16 * (r + 1)))) for r in range(len(qt.paths))]
+    qp = Plan(qp.jobs + tails, qp.method, qp.estimated_us, qp.settings)
+    a, b = prepare(qp, qq, large_min_tiles=1, fixed_from=t0), prepare(qp, qq, fixed_from=t0)
+    assert b.jobs == CachedDecodePlan(schedule(qt, 32, 8, 128, "cube", CostModel.mi355x()), qq, t0, 16).prepared.jobs
+    assert [(j.requests, j.tokens) for j in a.jobs] == [(j.requests, j.tokens) for j in b.jobs]
+    assert list(a.abi.n_items) == list(b.abi.n_items)

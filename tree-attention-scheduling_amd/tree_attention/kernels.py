@@ -193,6 +193,12 @@ FUSE_ROWS = 256
 # the 13 layers it changes, 0.78x at best)
 TAIL_KEEP_TILES = 1
 TAIL_KEEP_ITEMS_PER_CU = 4
+# large chunks are at least this many tiles long when that keeps the lowering's kernel
+# kinds and attachments and still gives half a work item per CU: a work item's time is
+# mostly its start-up latency, and every chunk is one more partial slot to merge
+# (measured: 0.986x on the 81-shape grid, 0.997x on the reference's 81 trees, 0.89x on
+# the benchmark case "wide" of 32 requests over 2048 shared tokens)
+LARGE_MIN_TILES = 2
 # wider large jobs run as 64-row request groups when 64-row items run anyway and no wider
 # job exceeds this many rows (prepare's consolidate_rows; 0: never)
 CONSOLIDATE_ROWS = 128
@@ -340,14 +346,15 @@ def _fuse_same_tokens(jobs, group, min_rows):
     return out
 
 
-def _recut(jobs, items_per_chunk, target_items, is_fixed):
+def _recut(jobs, items_per_chunk, target_items, is_fixed, min_tiles=1, floor_items=0):
     """Execution jobs for one kernel kind: runs of consecutive jobs over the same
     requests and contiguous tokens are cut again into near-equal chunks, as long
     as possible while the kind still gets ``target_items`` work items (one
     workgroup per CU for the large kinds).  Fewer, longer chunks mean fewer
     partial outputs to write and merge; the result is the same attention.
     Jobs for which ``is_fixed(job)`` holds (growing decode tails, tails that
-    merge their request) are left alone.
+    merge their request) are left alone.  Chunks are at least ``min_tiles``
+    tiles long whenever that still gives ``floor_items`` work items.
     """
     runs = []  # [requests, first token, length, fixed]
     for job in jobs:
@@ -381,6 +388,8 @@ def _recut(jobs, items_per_chunk, target_items, is_fixed):
             lo = mid
         else:
             hi = mid
+    if lo < min_tiles and count(min_tiles * TOKEN_QUANTUM) >= floor_items:
+        lo = min_tiles
     limit = lo * TOKEN_QUANTUM
     out = []
     for reqs, t0, n, fixed in runs:
@@ -526,7 +535,8 @@ def _metadata_numpy(jobs, small_jobs, nreq, group, kvheads, tile_rows, attached,
 
 def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int | None = None,
             attach_tails: bool = True, route_items: int = ROUTE_ITEMS, fuse_rows: int = FUSE_ROWS,
-            consolidate_rows: int = CONSOLIDATE_ROWS) -> PreparedPlan:
+            consolidate_rows: int = CONSOLIDATE_ROWS, large_target: int | None = None,
+            small_target: int | None = None, large_min_tiles: int = LARGE_MIN_TILES) -> PreparedPlan:
     """Lower ``plan`` to device metadata and scratch for queries shaped like ``q``.
 
     Mirrors kernels.py:103-141: physical jobs, stable small-first order, one
@@ -542,7 +552,12 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     tails are then in ``attached``, not in ``jobs``.  When small jobs are left for
     the small-job kernel and the large jobs, cut into 16-row request groups, stream
     at most ``route_items`` (tile, KV head) units, the large jobs run as those
-    groups in the small-job kernel instead (one segment launch less).  Raises
+    groups in the small-job kernel instead (one segment launch less).
+    ``large_target`` and ``small_target`` are the work items the re-cut aims at
+    for the large kinds and the small-job kind (default: one and eight per CU).
+    Large chunks of one tile are lengthened to ``large_min_tiles`` tiles when
+    that keeps the kernel kinds and the attachments and gives at least half of
+    ``large_target`` work items.  Raises
     ``ValueError`` for jobs without requests or tokens, request ids outside
     ``q`` and token runs that are not consecutive physical ids.
     """
@@ -571,14 +586,16 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
         if per and small and large else []
     small0 = small
     n_cu = _cu_count(q.device)
+    large_target = n_cu if large_target is None else large_target
+    small_target = 8 * n_cu if small_target is None else small_target
 
     def growing(job):
         return fixed_from is not None and job.tokens[0] >= fixed_from
 
-    def lower(small, large):
+    def lower(small, large, min_tiles):
         """Re-cut, order and attach: (small jobs, large jobs, attachments)."""
         large = _recut(large, lambda r: -(-len(r) * group // _native.KIND_ROWS[_large_kind(len(r) * group, tile_rows)])
-                       * kvheads, n_cu, growing)
+                       * kvheads, large_target, growing, min_tiles, large_target // 2)
         # chunks of one token range side by side: a root split into request groups then gives
         # request r its k-th slot at r + k * (requests of a chunk), the layout the merge computes
         large.sort(key=lambda j: (j.tokens[0], j.requests[0]))
@@ -597,26 +614,41 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
                 large = [j for j in large if id(j) not in gone]
         return small, large, attached
 
+    def lowering(min_tiles):
+        """``lower``, then one large-job kind and routing: (small, large, attachments)."""
+        small, large, attached = lower(small0, large0, min_tiles)
+        # One large-job kind: when 64-row items run anyway and every wider job holds at most
+        # consolidate_rows rows, the wider jobs run as 64-row request groups in the same kind
+        # (one launch and its start-up less; their K/V is read once per group).
+        per64 = 64 // group
+        wide = [j for j in large0 if len(j.requests) * group > 64]
+        if (consolidate_rows and per64 and wide and all(len(j.requests) * group <= consolidate_rows for j in wide)
+                and any(_large_kind(len(j.requests) * group, tile_rows) == _native.TA_LARGE64 for j in large)):
+            split = []
+            for j in large0:
+                if len(j.requests) * group > 64:
+                    split += [Job(j.requests[i:i + per64], j.tokens) for i in range(0, len(j.requests), per64)]
+                else:
+                    split.append(j)
+            # a last group of at most 16 rows is a small job
+            small, large, attached = lower(small0 + [j for j in split if len(j.requests) * group <= SMALL_ROWS],
+                                           [j for j in split if len(j.requests) * group > SMALL_ROWS], min_tiles)
+        if small and routed and sum(map(_tiles, routed)) * kvheads <= route_items:
+            small, large, attached = small0 + routed, [], {}
+        return small, large, attached
+
+    def kinds(small, large):
+        return ({-1} if small else set()) | {_large_kind(len(j.requests) * group, tile_rows) for j in large}
+
     large0 = large
-    small, large, attached = lower(small0, large0)
-    # One large-job kind: when 64-row items run anyway and every wider job holds at most
-    # consolidate_rows rows, the wider jobs run as 64-row request groups in the same kind
-    # (one launch and its start-up less; their K/V is read once per group).
-    per64 = 64 // group
-    wide = [j for j in large0 if len(j.requests) * group > 64]
-    if (consolidate_rows and per64 and wide and all(len(j.requests) * group <= consolidate_rows for j in wide)
-            and any(_large_kind(len(j.requests) * group, tile_rows) == _native.TA_LARGE64 for j in large)):
-        split = []
-        for j in large0:
-            if len(j.requests) * group > 64:
-                split += [Job(j.requests[i:i + per64], j.tokens) for i in range(0, len(j.requests), per64)]
-            else:
-                split.append(j)
-        # a last group of at most 16 rows is a small job
-        small, large, attached = lower(small0 + [j for j in split if len(j.requests) * group <= SMALL_ROWS],
-                                       [j for j in split if len(j.requests) * group > SMALL_ROWS])
-    if small and routed and sum(map(_tiles, routed)) * kvheads <= route_items:
-        small, large, attached = small0 + routed, [], {}
+    small, large, attached = lowering(1)
+    if large_min_tiles > 1 and any(len(j.tokens) < large_min_tiles * TOKEN_QUANTUM for j in large):
+        # A one-tile chunk costs a work item's start-up and a partial slot: chunks of
+        # large_min_tiles tiles are taken when the lowering keeps its kernel kinds and
+        # leaves no more small jobs (an item's latency, not its tiles, sets its time).
+        alt = lowering(large_min_tiles)
+        if kinds(*alt[:2]) == kinds(small, large) and len(alt[0]) <= len(small):
+            small, large, attached = alt
     # Tails (a request's only small job) stay whole when they alone fill the GPU,
     # so that their work items can merge their requests.
     owners = {}
@@ -629,7 +661,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     longest = max((_tiles(j) for j in tails), default=0)
     enough = len(tails) * kvheads >= n_cu * (1 if longest <= TAIL_KEEP_TILES else TAIL_KEEP_ITEMS_PER_CU)
     keep = {id(j) for j in tails} if enough else set()
-    small = _recut(small, lambda r: kvheads, 8 * n_cu, lambda j: growing(j) or id(j) in keep)
+    small = _recut(small, lambda r: kvheads, small_target, lambda j: growing(j) or id(j) in keep)
     jobs = small + large
     small_jobs = len(small)
     njobs = len(jobs)
@@ -688,7 +720,8 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
                         slots_t, counts_t, part, lse, out, rowbase_t, item_views, abi, metadata, rest_t,
                         keyed, xtail_t if attached else None, plan,
                         {"tile_rows": tile_rows, "fixed_from": fixed_from, "route_items": route_items, "fuse_rows": fuse_rows,
-                         "consolidate_rows": consolidate_rows}, None,
+                         "consolidate_rows": consolidate_rows, "large_target": large_target,
+                         "small_target": small_target, "large_min_tiles": large_min_tiles}, None,
                         meta["qbase"].tolist(),
                         grow_offsets=grow_offsets)
 
