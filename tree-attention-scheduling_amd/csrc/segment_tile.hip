@@ -39,6 +39,15 @@
 #include "ta_common.h"
 #include "tree_attn.h"
 
+// Work items that stream at most this many 64-token tiles store their partial
+// rows with the nontemporal hint (store_partial's `stream`).  Such items wait
+// on memory latency, and the end-of-kernel writeback of the partials dirty in
+// L2 lengthened their kernels; longer items keep plain stores, whose lines
+// leave L2 while the others still compute.
+#ifndef TA_STREAM_TILES
+#define TA_STREAM_TILES 8
+#endif
+
 namespace ta {
 namespace {
 
@@ -423,7 +432,7 @@ __device__ __forceinline__ void tile_item(const SegParams &p, const int32_t *__r
         if (grow >= nrows) continue;
         const int lr = grow / p.group, gg = grow - lr * p.group;
         const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
-        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4);
+        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4, ntiles <= TA_STREAM_TILES);
     }
 }
 
@@ -814,7 +823,7 @@ __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__r
         if (grow >= nrows) continue;
         const int lr = grow / p.group, gg = grow - lr * p.group;
         const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
-        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4);
+        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4, ntot <= TA_STREAM_TILES);
     }
 }
 
