@@ -473,8 +473,11 @@ __global__ __launch_bounds__(MERGE_NT) void merge_kernel(const u16 *__restrict__
         for (int u = 0; u < MERGE_CHUNK; ++u) {
             const int k = min(s0 + u, cnt - 1);
             const int sl = slot_stride > 0 ? r + k * slot_stride : slr[k];
-            le[u] = lse2[(size_t)sl * hq];
-            v[u] = *(const u32x4 *)(src + sl * srow);
+            // nontemporal: the partials are read once, and leaving them out of L2
+            // keeps the next segment launch's metadata, Q and code there
+            const f32x2 t = __builtin_nontemporal_load((const f32x2 *)(lse2 + (size_t)sl * hq));
+            le[u] = float2(t[0], t[1]);
+            v[u] = __builtin_nontemporal_load((const u32x4 *)(src + sl * srow));
         }
         float l[MERGE_CHUNK];
         float cm = M;
