@@ -392,14 +392,21 @@ def _recut(jobs, items_per_chunk, target_items, is_fixed, min_tiles=1, floor_ite
         lo = min_tiles
     limit = lo * TOKEN_QUANTUM
     out = []
+    # chunks are built field by field (what the frozen dataclass's __init__
+    # does) from slices of one id run: this loop makes most of prepare's jobs
+    new, put = object.__new__, object.__setattr__
     for reqs, t0, n, fixed in runs:
+        ids = id_run(t0, t0 + n)
         if fixed:
-            out.append(Job(reqs, id_run(t0, t0 + n)))
+            out.append(Job(reqs, ids))
             continue
         pieces = -(-n // limit)
         size = -(-(-(-n // pieces)) // 8) * 8  # near-equal, 8-token aligned
         for a in range(0, n, size):
-            out.append(Job(reqs, id_run(t0 + a, t0 + min(n, a + size))))
+            job = new(Job)
+            put(job, "requests", reqs)
+            put(job, "tokens", ids[a:a + size])
+            out.append(job)
     return out
 
 
