@@ -18,8 +18,9 @@
 //    and the waves meet at one barrier per tile.
 //  * The lane -> 16-byte-chunk assignment inside a block is chosen so that the
 //    eight chunks one 16-lane group reads together are 128 contiguous bytes,
-//    and blocks are padded to 1152 bytes so that neighbouring groups start
-//    128 bytes apart (no LDS bank conflicts on 32- or 64-bank LDS).
+//    and odd blocks swap the two 128-byte halves of every 256 bytes so that
+//    neighbouring groups land 128 bytes apart (no LDS bank conflicts; see
+//    the LDS layout note above struct LdsOfs).
 //  * MFMA operands are read with gfx950's transposing LDS load
 //    ds_read_b64_tr_b16: within a group of 16 lanes, lane 4a+b receives
 //    element b of the 8-byte chunks addressed by lanes a, a+4, a+8, a+12.
@@ -38,15 +39,6 @@
 // pools, so every 8-token chunk of a K row is one aligned 16-byte copy.
 #include "ta_common.h"
 #include "tree_attn.h"
-
-// Work items that stream at most this many 64-token tiles store their partial
-// rows with the nontemporal hint (store_partial's `stream`).  Such items wait
-// on memory latency, and the end-of-kernel writeback of the partials dirty in
-// L2 lengthened their kernels; longer items keep plain stores, whose lines
-// leave L2 while the others still compute.
-#ifndef TA_STREAM_TILES
-#define TA_STREAM_TILES 8
-#endif
 
 namespace ta {
 namespace {
@@ -432,7 +424,7 @@ __device__ __forceinline__ void tile_item(const SegParams &p, const int32_t *__r
         if (grow >= nrows) continue;
         const int lr = grow / p.group, gg = grow - lr * p.group;
         const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
-        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4, ntiles <= TA_STREAM_TILES);
+        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4);
     }
 }
 
@@ -823,7 +815,7 @@ __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__r
         if (grow >= nrows) continue;
         const int lr = grow / p.group, gg = grow - lr * p.group;
         const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
-        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4, ntot <= TA_STREAM_TILES);
+        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4);
     }
 }
 

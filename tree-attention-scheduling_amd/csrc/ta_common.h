@@ -94,12 +94,12 @@ __device__ inline u32 pack_f16(float lo, float hi) {
     return __builtin_bit_cast(u32, v);
 }
 
-// `stream` stores with the nontemporal hint: the lines go out during the
-// kernel instead of staying dirty in L2 until its end (taken by short work
-// items, whose kernel end waits for that writeback).
+// The stores carry the nontemporal hint: the partial lines leave L2 while the
+// kernel runs instead of waiting there, dirty, for the end-of-kernel writeback,
+// and the merge reads each of them once.
 template <int DB>
 __device__ inline void store_partial(u16 *part, float *lse2, size_t prow, const f32x4 (&o)[DB], float m, float z,
-                                     int g4, bool stream = false) {
+                                     int g4) {
     constexpr int D = 16 * DB;
     const bool any = m != NEG_INF;
     const float inv = any ? 1.f / z : 0.f;
@@ -121,25 +121,17 @@ __device__ inline void store_partial(u16 *part, float *lse2, size_t prow, const 
         w[db] = u32x2{pack_f16(v[0], v[1]), pack_f16(v[2], v[3])};
     }
     const float l = any ? (m + __builtin_amdgcn_logf(z)) * LN2 : NEG_INF;
-    if (stream) {
-        // the empty asm statements keep the two branches' stores apart: hoisted
-        // or sunk into one, they would lose the hint
-        asm volatile("" ::: "memory");
+    // The empty asm statements keep the stores together, after every
+    // conversion: left free, the compiler spread them among the conversions
+    // and the headline layer ran 6 % longer.
+    asm volatile("" ::: "memory");
 #pragma unroll
-        for (int db = 0; db < DB; ++db) __builtin_nontemporal_store(w[db], (u32x2 *)(dst + 16 * db));
-        if (g4 == 0) {
-            __builtin_nontemporal_store(l, lse2 + 2 * prow);
-            __builtin_nontemporal_store((float)e, lse2 + 2 * prow + 1);
-        }
-        asm volatile("" ::: "memory");
-    } else {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) *(u32x2 *)(dst + 16 * db) = w[db];
-        if (g4 == 0) {
-            lse2[2 * prow] = l;
-            lse2[2 * prow + 1] = (float)e;
-        }
+    for (int db = 0; db < DB; ++db) __builtin_nontemporal_store(w[db], (u32x2 *)(dst + 16 * db));
+    if (g4 == 0) {
+        __builtin_nontemporal_store(l, lse2 + 2 * prow);
+        __builtin_nontemporal_store((float)e, lse2 + 2 * prow + 1);
     }
+    asm volatile("" ::: "memory");
 }
 
 // Four fp16 partial values (8 bytes) -> floats.  The whole vector is
