@@ -22,7 +22,9 @@
  *       vp    [hk, tcap, d]        V pool                 (kernels.py:145, qwen.py:28)
  *       part  [nslot, hq, d] fp16  normalised partial output per (job, request),
  *                                  row-scaled: stored value = (o / z) * 2^-e with e
- *                                  the frexp exponent of the row's largest |o / z|
+ *                                  the frexp exponent of the row's largest |o / z|;
+ *                                  within a row, element d = 32p + 16h + 4g + i
+ *                                  (i < 4) is stored at 32p + 8g + 4h + i
  *       lse   [nslot, hq, 2] fp32  per row: natural-log log-sum-exp, then e
  *       out   [nreq, hq, d]
  *   - Job j covers physical tokens [kstart[j], kstart[j] + klen[j]) for the requests

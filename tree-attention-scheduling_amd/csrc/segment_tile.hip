@@ -950,7 +950,7 @@ __global__ __launch_bounds__(128) void seg_tail_kernel(SegParams p) {
             for (int k = 0; k < UPL; ++k) {
                 const int u = min(lane + 64 * k, units - 1);
                 const size_t prow = (size_t)sl * p.hq + h * G + u / DU;
-                const u32x2 x = *(const u32x2 *)(p.part + prow * D + 4 * (u % DU));
+                const u32x2 x = *(const u32x2 *)(p.part + prow * D + part_pos(u % DU));
                 const float lx = p.lse[2 * prow], ex = p.lse[2 * prow + 1];
                 l[c][k] = use ? lx * LOG2E : NEG_INF;
                 e[c][k] = (int)ex;

@@ -89,6 +89,13 @@ __device__ inline float xor_sum(float v) {
 // log-sum-exp of the row and lse2[2 prow + 1] = e.  Lane (row, g4) of a
 // 16-row MFMA block holds d = 16 db + 4 g4 + i in o[db][i]; the four lanes of
 // a row (g4 = 0..3, lanes 16 apart) must all be active.
+//
+// Within a row the values are stored in the lanes' order: head-dim element
+// d = 32 P + 16 h + 4 g + i (i < 4) sits at position 32 P + 8 g + 4 h + i, so
+// that a lane writes d blocks 2P and 2P+1 as one 16-byte store and the four
+// lanes of a row fill whole 64-byte lines.  part_pos gives the position of
+// the four-element chunk starting at d = 4 c.
+__device__ constexpr int part_pos(int c) { return 32 * (c >> 3) + 8 * (c & 3) + 4 * ((c >> 2) & 1); }
 __device__ inline u32 pack_f16(float lo, float hi) {
     f16x2 v = {(_Float16)lo, (_Float16)hi};
     return __builtin_bit_cast(u32, v);
@@ -113,12 +120,13 @@ __device__ inline void store_partial(u16 *part, float *lse2, size_t prow, const 
     amax = fmaxf(amax, __shfl_xor(amax, 32));
     const int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
     const float s = __builtin_amdgcn_ldexpf(inv, -e);
-    u16 *dst = part + prow * D + 4 * g4;
-    u32x2 w[DB];
+    static_assert(DB % 2 == 0, "d blocks are stored in pairs");
+    u16 *dst = part + prow * D + 8 * g4;
+    u32x4 w[DB / 2];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        const f32x4 v = o[db] * s;
-        w[db] = u32x2{pack_f16(v[0], v[1]), pack_f16(v[2], v[3])};
+    for (int pr = 0; pr < DB / 2; ++pr) {
+        const f32x4 a = o[2 * pr] * s, b = o[2 * pr + 1] * s;
+        w[pr] = u32x4{pack_f16(a[0], a[1]), pack_f16(a[2], a[3]), pack_f16(b[0], b[1]), pack_f16(b[2], b[3])};
     }
     const float l = any ? (m + __builtin_amdgcn_logf(z)) * LN2 : NEG_INF;
     // The empty asm statements keep the stores together, after every
@@ -126,7 +134,7 @@ __device__ inline void store_partial(u16 *part, float *lse2, size_t prow, const 
     // and the headline layer ran 6 % longer.
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int db = 0; db < DB; ++db) __builtin_nontemporal_store(w[db], (u32x2 *)(dst + 16 * db));
+    for (int pr = 0; pr < DB / 2; ++pr) __builtin_nontemporal_store(w[pr], (u32x4 *)(dst + 32 * pr));
     if (g4 == 0) {
         __builtin_nontemporal_store(l, lse2 + 2 * prow);
         __builtin_nontemporal_store((float)e, lse2 + 2 * prow + 1);

@@ -508,9 +508,10 @@ __global__ __launch_bounds__(MERGE_NT) void merge_kernel(const u16 *__restrict__
         lo *= inv;
         hi *= inv;
     }
-    u16 *dst = out + ((size_t)r * hq + head) * D + 8 * d8;
-    *(u32x4 *)dst = u32x4{Ops<FP16>::pack(lo[0], lo[1]), Ops<FP16>::pack(lo[2], lo[3]), Ops<FP16>::pack(hi[0], hi[1]),
-                          Ops<FP16>::pack(hi[2], hi[3])};
+    // the slice holds d = 32 (d8 / 4) + 4 (d8 % 4) + {0..3} (lo) and the same + 16 (hi)
+    u16 *dst = out + ((size_t)r * hq + head) * D + 32 * (d8 >> 2) + 4 * (d8 & 3);
+    *(u32x2 *)dst = u32x2{Ops<FP16>::pack(lo[0], lo[1]), Ops<FP16>::pack(lo[2], lo[3])};
+    *(u32x2 *)(dst + 16) = u32x2{Ops<FP16>::pack(hi[0], hi[1]), Ops<FP16>::pack(hi[2], hi[3])};
 }
 
 // ------------------------------------------------------------------ read ceiling
