@@ -146,6 +146,23 @@ def test_nested_unequal_tree(device):
             check(out, ref, 0.008, 0.03, f"nested/{method}")
 
 
+@pytest.mark.parametrize("hq,hk,d", [(8, 2, 32), (8, 2, 64), (32, 8, 128)])
+def test_merge_of_many_slots(hq, hk, d, device):
+    """More than 16 partial slots per request (the merge splits them into two ranges), ragged counts
+    (11 to 45 slots), and 8 query heads, which fill only part of a merge workgroup at d = 32 and 64."""
+    tree = shapes.tree(shapes.shared_prefix(6, 700, [1, 33, 900, 17, 2130, 64]))
+    q, k, v = make_inputs(tree, hq, hk, d, torch.bfloat16, 5)
+    ref = oracle_fp32(q, k, v, tree)
+    model = CostModel(kv_split=64)
+    plan = schedule(tree, hq, hk, d, "request", model)
+    counts = prepare(plan, q.to(device)).counts.cpu()
+    assert counts.max() > 16 and counts.min() < 16 and counts.max() % 2 == 1, counts
+    for method in METHODS:
+        say("many-slots", hq, hk, d, method)
+        out = run(tree, method, model, q, k, v, device, (hq, hk, d))
+        check(out, ref, 0.008, 0.03, f"many-slots{hq}/{d}/{method}")
+
+
 @pytest.mark.parametrize("hq,hk", [(8, 8), (16, 2), (32, 2), (64, 4)])
 def test_group_sizes(hq, hk, device):
     """GQA group sizes 1, 8, 16, 16 (rows per request up to one full 16-row block)."""

@@ -444,34 +444,50 @@ __global__ __launch_bounds__(64 * NW) void seg_large_kernel(SegParams p) {
 constexpr int MERGE_CHUNK = 16;
 constexpr int MERGE_NT = 128;
 
-template <int D, bool FP16>
-__global__ __launch_bounds__(MERGE_NT) void merge_kernel(const u16 *__restrict__ part, const float *__restrict__ lse,
-                                                         const int32_t *__restrict__ slots,
-                                                         const int32_t *__restrict__ counts,
-                                                         const int32_t *__restrict__ reqs, u16 *__restrict__ out,
-                                                         int hq, int maxs, int slot_stride) {
+// SPLIT groups of MERGE_NT threads split a request's slots into SPLIT
+// contiguous ranges, merge them side by side (one round trip of loads per
+// MERGE_CHUNK slots each) and combine their running (max, sum, partial sums)
+// through LDS; the first group writes the output.  SPLIT = 2 serves plans with
+// more than MERGE_CHUNK slots per request: 32 slots wait for one round of loads
+// instead of two.  SPLIT = 1 is the single-group kernel described above.
+template <int D, bool FP16, int SPLIT>
+__global__ __launch_bounds__(MERGE_NT * SPLIT) void merge_kernel(const u16 *__restrict__ part,
+                                                                 const float *__restrict__ lse,
+                                                                 const int32_t *__restrict__ slots,
+                                                                 const int32_t *__restrict__ counts,
+                                                                 const int32_t *__restrict__ reqs,
+                                                                 u16 *__restrict__ out, int hq, int maxs,
+                                                                 int slot_stride) {
     constexpr int TPH = D / 8;          // threads per head
     constexpr int MH = MERGE_NT / TPH;  // heads per workgroup
     constexpr float LOG2E = 1.44269504088896341f;
     const int r = reqs ? reqs[blockIdx.x] : blockIdx.x;
-    const int tid = threadIdx.x;
+    // a group is whole waves: readfirstlane tells the compiler grp is uniform
+    const int grp = SPLIT > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x / MERGE_NT) : 0;
+    const int tid = threadIdx.x % MERGE_NT;
     const int hl = tid / TPH, d8 = tid % TPH;
     const int head = blockIdx.y * MH + hl;
-    if (head >= hq) return;
+    const bool valid = head < hq;
+    if (SPLIT == 1 && !valid) return;
     const int cnt = slot_stride > 0 ? maxs : counts[r];
+    const int per = (cnt + SPLIT - 1) / SPLIT;
+    const int beg = SPLIT > 1 ? min(cnt, grp * per) : 0, end = SPLIT > 1 ? min(cnt, beg + per) : cnt;
+    const int hr = SPLIT > 1 ? min(head, hq - 1) : head;  // the head this lane reads
     const int32_t *slr = slots + (size_t)r * maxs;
-    const u16 *src = part + (size_t)head * D + 8 * d8;
-    const float2 *lse2 = reinterpret_cast<const float2 *>(lse) + head;
+    const u16 *src = part + (size_t)hr * D + 8 * d8;
+    const float2 *lse2 = reinterpret_cast<const float2 *>(lse) + hr;
     const size_t srow = (size_t)hq * D;
 
     float M = NEG_INF, Z = 0.f;  // running max (log2 units) and weight sum
     f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
-    for (int s0 = 0; s0 < cnt; s0 += MERGE_CHUNK) {
+    // the loop bounds stay uniform (so the slot list is read by scalar loads):
+    // lanes past hq read head hq - 1 and store nothing
+    for (int s0 = beg; s0 < end; s0 += MERGE_CHUNK) {
         float2 le[MERGE_CHUNK];
         u32x4 v[MERGE_CHUNK];
 #pragma unroll
         for (int u = 0; u < MERGE_CHUNK; ++u) {
-            const int k = min(s0 + u, cnt - 1);
+            const int k = min(s0 + u, end - 1);
             const int sl = slot_stride > 0 ? r + k * slot_stride : slr[k];
             // nontemporal: the partials are read once, and leaving them out of L2
             // keeps the next segment launch's metadata, Q and code there
@@ -483,7 +499,7 @@ __global__ __launch_bounds__(MERGE_NT) void merge_kernel(const u16 *__restrict__
         float cm = M;
 #pragma unroll
         for (int u = 0; u < MERGE_CHUNK; ++u) {
-            l[u] = s0 + u < cnt ? le[u].x * LOG2E : NEG_INF;
+            l[u] = s0 + u < end ? le[u].x * LOG2E : NEG_INF;
             cm = fmaxf(cm, l[u]);
         }
         if (cm == NEG_INF) continue;  // every slot so far is empty
@@ -501,6 +517,36 @@ __global__ __launch_bounds__(MERGE_NT) void merge_kernel(const u16 *__restrict__
             const float ws = __builtin_amdgcn_ldexpf(w, (int)le[u].y);
             lo += ws * unpack_f16x4(u32x2{v[u][0], v[u][1]});
             hi += ws * unpack_f16x4(u32x2{v[u][2], v[u][3]});
+        }
+    }
+    if constexpr (SPLIT > 1) {
+        __shared__ float sh[SPLIT - 1][10][MERGE_NT];
+        if (grp > 0) {
+            float *x = &sh[grp - 1][0][tid];
+            x[0] = M;
+            x[MERGE_NT] = Z;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[(2 + i) * MERGE_NT] = lo[i];
+                x[(6 + i) * MERGE_NT] = hi[i];
+            }
+        }
+        __syncthreads();
+        if (grp > 0 || !valid) return;
+#pragma unroll
+        for (int g = 0; g < SPLIT - 1; ++g) {
+            const float *x = &sh[g][0][tid];
+            const float Mg = x[0];
+            if (Mg == NEG_INF) continue;  // an empty range
+            const float cm = fmaxf(M, Mg);
+            const float alpha = fast_exp2(M - cm), beta = fast_exp2(Mg - cm);  // alpha is 0 while M is -inf
+            Z = Z * alpha + x[MERGE_NT] * beta;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                lo[i] = lo[i] * alpha + x[(2 + i) * MERGE_NT] * beta;
+                hi[i] = hi[i] * alpha + x[(6 + i) * MERGE_NT] * beta;
+            }
+            M = cm;
         }
     }
     if (Z > 0.f) {
@@ -577,8 +623,14 @@ hipError_t launch_merge(const void *part, const float *lse, const int32_t *slots
                         const int32_t *reqs, void *out, int nreq, int hq, int maxs, hipStream_t stream,
                         int slot_stride = 0) {
     constexpr int MH = MERGE_NT / (D / 8);
-    TA_LAUNCH((merge_kernel<D, FP16>), dim3(nreq, (hq + MH - 1) / MH), dim3(MERGE_NT), stream,
-              static_cast<const u16 *>(part), lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs, slot_stride);
+    if (maxs > MERGE_CHUNK)
+        TA_LAUNCH((merge_kernel<D, FP16, 2>), dim3(nreq, (hq + MH - 1) / MH), dim3(2 * MERGE_NT), stream,
+                  static_cast<const u16 *>(part), lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs,
+                  slot_stride);
+    else
+        TA_LAUNCH((merge_kernel<D, FP16, 1>), dim3(nreq, (hq + MH - 1) / MH), dim3(MERGE_NT), stream,
+                  static_cast<const u16 *>(part), lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs,
+                  slot_stride);
     return hipGetLastError();
 }
 
