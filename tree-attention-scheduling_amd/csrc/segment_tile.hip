@@ -435,430 +435,167 @@ __global__ __launch_bounds__(64 * NW) void seg_tile_kernel(SegParams p) {
 }
 
 // ------------------------------------------------------------------------
-// Pipelined 256-row kernel (kind TA_LARGE256) on 32x32x16 MFMAs.
+// Pipelined large-tile kernel.  The 32-token steps of a work item form one
+// software pipeline that runs across tile boundaries; within a step the
+// matrix cores and the VALU work on different steps:
 //
-// Eight waves own 32 query rows each -- one N block of
-// v_mfma_f32_32x32x16_{bf16,f16} -- and share every staged K/V tile.  Per
-// 32-token step a wave runs D/16 QK MFMAs (S^T = K Q^T, tokens x rows), D/16
-// PV MFMAs (O^T = V^T P^T, d x rows) and two 16x16x32 MFMAs for the softmax
-// denominator.  A 32x32 MFMA occupies the matrix core twice as long as a
-// 16x16 one and hides about three times the VALU work behind it (measured on
-// gfx950: 24 cycles per 32x32 MFMA, 8 per 16x16), which is what the
-// exponentials, conversions and maxima of a step need.
+//   block(g):  QK of step g+1 (MFMA)   || exponentials of step g (VALU),
+//                                          LDS reads of V(g)
+//              PV + row sums of step g  || LDS reads of K(g+2), masking and
+//                                          row maxima of step g+1
 //
-// The steps form one software pipeline across tile boundaries:
-//
-//   block(g):  QK of step g+1 (MFMA)   || exponentials and bf16/f16 packing
-//                                         of step g, LDS reads of V(g)
-//              PV + denominator of g   || LDS reads of K(g+2), masking, row
-//                                         maxima and c*s - m of step g+1
-//
-// The shifted scores t = c*s - m are formed with the running maximum m
-// before the lazy-rescale check of their step; when the check raises m (a
-// wave-uniform branch, rare after the first step) t is moved by the change
-// of m.  The order inside a block is pinned with sched_group_barrier.  K/V
-// tiles arrive by LDS DMA into five stages: tiles t and t+1 are read while
-// t+2 .. t+4 are in flight, with one barrier per tile.
+// and the rare online-softmax rescale runs between blocks.  The order inside
+// a block is pinned with sched_group_barrier so that MFMAs and VALU
+// instructions alternate in each wave's instruction stream.  K/V tiles arrive
+// by LDS DMA into five stages: tiles t and t+1 are read while t+2 .. t+4 are
+// in flight, with one barrier per tile.
+template <int D, bool FP16, int NW, int NB_ = 2>
+struct PipeMath {
+    static constexpr int NB = NB_;
+    static constexpr int DB = D / 16;
+    static constexpr int KS = D / 32;
+    using O = Ops<FP16>;
+    using T = Tile<D>;
+    using TM = TileMath<D, FP16, NB, NW>;
 
-// LDS layout of one 64-token tile for the 32-row kernel (16-bit elements):
-// KBLK 1 KiB blocks of K, then VBLK of V, each a copy unit of 64 16-byte
-// slots (one slot per lane of the copying wave).
-//   K block b: d-rows 8b + j (j < 8); chunk c (tokens 8c .. 8c+7, c < 8) of
-//     d-row 8b + j sits at slot 16u + 8((j >> 2) ^ (u & 1)) + 4(c & 1) +
-//     (j & 3), u = c >> 1: a transposing read of 4 d-rows x 16 tokens is one
-//     128-byte run, and runs of adjacent 16-token units lie in opposite
-//     halves of 256 bytes.
-//   V block vb: token rows VROWS vb + jr; a 128-byte unit holds 4 token rows
-//     (row quad rq = jr >> 2) x 16 d (unit du = d >> 4) as slots 4 (s & 1) +
-//     (jr & 3) for chunk s = d >> 3; unit (rq, du) sits at 128 bytes x
-//     vunit(rq, du), whose low bit is (du ^ rq) & 1.
-// The four 16-lane groups of a transposing read each take one 128-byte run;
-// groups 0/1 and 2/3 land in opposite 128-byte halves of the 64 banks.
-template <int D>
-struct Tile32 {
-    static constexpr int TT = 64;
-    static constexpr int BLK = 512;
-    static constexpr int KBLK = D / 8;
-    static constexpr int VROWS = 512 / D;
-    static constexpr int VBLK = TT / VROWS;
-    static constexpr int NBLK = KBLK + VBLK;
-    static constexpr int ELEMS = NBLK * BLK;
-    static constexpr int NDU = D / 16;  // 16-d units of a V row
-    static_assert(D % 32 == 0 && D <= 128, "d = 32, 64 or 128");
-
-    __host__ __device__ static constexpr int vunit(int rq, int du) {
-        return ((rq * NDU + du) & ~1) | ((du ^ rq) & 1);
-    }
-    // element offset, within the tile, of the 128-byte V run read by group
-    // g's lanes for token rows tau .. tau+3 (tau % 4 == 0) and d unit du
-    __host__ __device__ static constexpr int vrun(int tau, int du) {
-        return BLK * (KBLK + tau / VROWS) + 64 * vunit((tau % VROWS) >> 2, du);
-    }
-    // V read of step base sb, 16-token sub-block sub, run r (tokens 8r ..)
-    // and d tile dt, relative to the same read at (0, 0, 0, 0); the same for
-    // every lane group
-    __host__ __device__ static constexpr int vdelta(int sb, int sub, int r, int dt) {
-        return vrun(sb + 16 * sub + 8 * r, 2 * dt) - vrun(0, 0);
-    }
-};
-
-// Per-lane constants of one wave's tile copies and transposing reads.
-struct Lane32 {
-    int kdma;  // K copy: element offset j * tcap + 8c of this lane's slot
-    int vdma;  // V copy: element offset jr * D + 8s of this lane's slot
-    int kof0, kof1;  // K reads: element offsets of the two 4-d-row halves
-    int vof;         // V reads: element offset at (sb, sub, r, dt) = 0
-};
-
-template <int D, bool FP16>
-struct Pipe32 {
-    static constexpr int DT = D / 32;  // 32-row d tiles of O^T
-    static constexpr int KS = D / 16;  // 16-wide d slices of QK
-    using T = Tile32<D>;
-
-    f32x16 o[DT];
-    f32x4 z;        // denominators: lane r < 16 holds row r (z[0]) and row r + 16 (z[1])
-    float m, thr, lm;  // per lane (row lane % 32): running max (scaled), (m + TAU) / c, raw max of the next step
-    f32x16 s;       // shifted scores c*s - m of the step whose exponentials come next
-    u32x4 kf[KS];   // K fragments of the next QK step
-    u32x4 vf[2 * DT];  // V^T fragments of the current PV step: [2 dt + sub]
-
-    __device__ static f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
-        if constexpr (FP16)
-            return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
-                                                          c, 0, 0, 0);
-        else
-            return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                           __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    }
-
-    __device__ static Lane32 lane_consts(int lane, int tcap) {
-        Lane32 c;
-        {  // K copy: slot lane <- chunk c of d-row j
-            const int u = lane >> 4, h = ((lane >> 3) & 1) ^ (u & 1);
-            const int ch = 2 * u + ((lane >> 2) & 1), j = 4 * h + (lane & 3);
-            c.kdma = j * tcap + 8 * ch;
-        }
-        {  // V copy: slot lane <- chunk s of token row jr
-            const int uidx = lane >> 3, sin = lane & 7;
-            const int lin_hi = uidx & ~1, rq = lin_hi / T::NDU;
-            const int du = ((lin_hi % T::NDU) & ~1) | ((uidx & 1) ^ (rq & 1));
-            c.vdma = (4 * rq + (sin & 3)) * D + 8 * (2 * du + (sin >> 2));
-        }
-        const int g = lane >> 4, i = lane & 15;
-        const int in = 32 * ((i >> 1) & 1) + 8 * (i >> 2) + 4 * (i & 1);  // within a 128-byte run
-        c.kof0 = T::BLK * (g >> 1) + 128 * (g & 1) + 64 * (g & 1) + in;
-        c.kof1 = T::BLK * (g >> 1) + 128 * (g & 1) + 64 * (1 - (g & 1)) + in;
-        c.vof = T::vrun(4 * (g >> 1), g & 1) + in;
-        return c;
-    }
-
-    // Copy the tile at pool token t0n into stage `st` (this wave's blocks of
-    // NW waves).  Inside the job (tokens [t0n, t0n + TT) all in [kst, kend))
-    // no index is clamped; at its edges chunks past the pool end read its
-    // last chunk and V rows outside the job read a row inside it (finite
-    // values; their scores are masked, P = 0).
-    template <int NW>
-    __device__ static void copy(u16 *st, const u16 *__restrict__ kp, const u16 *__restrict__ vp, int h, int tcap,
-                                int t0n, int kst, int kend, int wave, int lane, const Lane32 &lc) {
-        const int w = __builtin_amdgcn_readfirstlane(wave);
-        if (t0n >= kst && t0n + T::TT <= kend)
-            copy_blocks<NW, false>(st, kp, vp, h, tcap, t0n, kst, kend, w, lane, lc);
-        else
-            copy_blocks<NW, true>(st, kp, vp, h, tcap, t0n, kst, kend, w, lane, lc);
-    }
-
-    template <int NW, bool CLAMP>
-    __device__ static void copy_blocks(u16 *st, const u16 *__restrict__ kp, const u16 *__restrict__ vp, int h,
-                                       int tcap, int t0n, int kst, int kend, int w, int lane, const Lane32 &lc) {
-        static_assert(T::NBLK % NW == 0, "every wave copies the same number of blocks");
-#pragma unroll
-        for (int i = 0; i < T::NBLK / NW; ++i) {
-            const int blk = w + i * NW;
-            const bool isk = T::KBLK % NW == 0 ? i * NW < T::KBLK : blk < T::KBLK;
-            const u16 *src;
-            if (isk) {
-                const u16 *base = kp + (size_t)(h * D + 8 * blk) * tcap;
-                if (CLAMP) {
-                    const int u = lane >> 4, hh = ((lane >> 3) & 1) ^ (u & 1);
-                    const int tok = t0n + 8 * (2 * u + ((lane >> 2) & 1));
-                    src = base + (size_t)(4 * hh + (lane & 3)) * tcap + min(tok, tcap - 8);
-                } else {
-                    src = base + t0n + lc.kdma;
-                }
-            } else {
-                const int t0 = t0n + T::VROWS * (blk - T::KBLK);
-                if (CLAMP) {
-                    const int jr = lc.vdma / D;
-                    const int t = min(max(t0 + jr, kst), kend - 1);
-                    src = vp + ((size_t)h * tcap + t) * D + (lc.vdma - jr * D);
-                } else {
-                    src = vp + ((size_t)h * tcap + t0) * D + lc.vdma;
-                }
-            }
-            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(st + blk * T::BLK), 16, 0, 0);
-        }
-    }
+    f32x4 o[NB][DB], z[NB];
+    float m[NB], lm[NB], thr[NB];  // running max (scaled), raw row max of the staged step, (m + TAU) / c
+    f32x4 s[NB][2];      // scores of the step whose exponentials come next
+    u32x4 kf[2][KS];     // K fragments of the next QK step
+    u32x4 vf[DB];        // V^T fragments of the current PV step
 
     __device__ void reset() {
-        m = thr = lm = NEG_INF;
-        z = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+        for (int nb = 0; nb < NB; ++nb) {
+            m[nb] = thr[nb] = NEG_INF;
+            z[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
-    }
-
-    // K fragments (A operand of QK) of the 32 tokens at step base sb (0 or
-    // 32) of the tile in `st`: kf[ks] covers d = 16 ks .. +15.
-    __device__ static void load_k(const u16 *__restrict__ st, const Lane32 &lc, int sb, u32x4 (&kf)[KS]) {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int e = 2 * T::BLK * ks + 8 * sb;
-            kf[ks] = tr_pair(st + lc.kof0 + e, st + lc.kof1 + e);
+            for (int db = 0; db < DB; ++db) o[nb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
 
-    // S^T = K Q^T of one step: lane l holds query row l % 32 and tokens
-    // 8 (e >> 2) + 4 (l >> 5) + (e & 3) in element e.
-    __device__ static f32x16 qk(const u32x4 (&kf)[KS], const u32x4 (&qf)[KS]) {
-        f32x16 acc;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) acc = mma32(kf[ks], qf[ks], acc);
-        return acc;
-    }
-
-    // Mask tokens outside [lo, hi) of the step (if MASK) and take the lane's
-    // raw row maximum.
+    // Scores of a step: mask tokens outside [lo, hi) (if MASK) and take the
+    // lane-local row maxima.
     template <bool MASK>
-    __device__ void mask_max(f32x16 &sn, int lo, int hi, int hf) {
-        if (MASK) {
+    __device__ void finish_scores(f32x4 (&sn)[NB][2], int lo, int hi, int g4) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int tok = 8 * (e >> 2) + 4 * hf + (e & 3);
-                if (tok < lo || tok >= hi) sn[e] = NEG_INF;
+        for (int nb = 0; nb < NB; ++nb) {
+            if (MASK) {
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int tok = 16 * b + 4 * g4 + i;
+                        if (tok < lo || tok >= hi) sn[nb][b][i] = NEG_INF;
+                    }
             }
-        }
-        float mx = sn[0];  // a chain, so that it becomes three-input maxima
+            float mx = sn[nb][0][0];  // a chain, so that it becomes three-input maxima
 #pragma unroll
-        for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sn[e]);
-        lm = mx;
-    }
-
-    __device__ void shift(const f32x16 &sn, float c) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[e] = __builtin_fmaf(sn[e], c, -m);
-    }
-
-    __device__ void scale(float alpha) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-        z[0] *= alpha;
-        z[1] *= __shfl_xor(alpha, 16);  // lanes r < 16: alpha of row r + 16
-    }
-
-    // Raise the running maxima where the staged step's raw maximum exceeds
-    // them by more than TAU (wave-uniform).  SHIFTED: s already holds
-    // c*s - m_old and is moved to c*s - m_new; otherwise the caller shifts.
-    template <bool SHIFTED>
-    __device__ void rescale(float c, float rc) {
-        if (__builtin_amdgcn_ballot_w64(lm > thr)) {
-            const float mn = fmaxf(m, fmaxf(lm, __shfl_xor(lm, 32)) * c);
-            if (SHIFTED) {
-                // m is finite here (the first step of an item is never shifted)
-                const float dm = m - mn;
-                scale(fast_exp2(dm));
-#pragma unroll
-                for (int e = 0; e < 16; ++e) s[e] += dm;
-            } else {
-                scale(mn == NEG_INF ? 1.f : fast_exp2(m - mn));
-            }
-            m = mn;
-            thr = (mn + TAU) * rc;
+            for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sn[nb][i >> 2][i & 3]);
+            lm[nb] = mx;
+            s[nb][0] = sn[nb][0];
+            s[nb][1] = sn[nb][1];
         }
     }
 
-    // One pipeline block (see above), written as slices of one MFMA each with
-    // the work that goes out beside it; a scheduling barrier between slices
-    // keeps that order (left free, the compiler issued the QK MFMAs back to
-    // back and the exponentials after them).
-    //   vsp / vsb: V(g) stage + this lane's V offset, and the step base;
-    //   ksp0 / ksp1 / ksb: K(g+2) stage + this lane's two K offsets, step base
-    //     (any resident step when there is none);
-    //   lo / hi: valid tokens of step g+1;  ROWMASK: only this lane's row if keep.
+    // Raise the running maxima where a score of the staged step exceeds them
+    // by more than TAU (wave-uniform branch, rare after the first step).
+    __device__ void rescale(float c, float rc) {  // rc = 1 / c
+        bool need = false;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) need |= lm[nb] > thr[nb];
+        if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const float mn = fmaxf(m[nb], xor_max(lm[nb]) * c);
+                const float alpha = mn == NEG_INF ? 1.f : fast_exp2(m[nb] - mn);
+                z[nb] *= alpha;
+#pragma unroll
+                for (int db = 0; db < DB; ++db) o[nb][db] *= alpha;
+                m[nb] = mn;
+                thr[nb] = (mn + TAU) * rc;  // raw-score threshold of the next rescale
+            }
+        }
+    }
+
+    // One pipeline block (see above).  vs / vbase: stage and offset of V(g);
+    // ks / kbase: of K(g+2) (any resident step when there is none); lo / hi:
+    // valid tokens of step g+1.  Every fragment register set is reloaded only
+    // after its last reader: V(g) during QK(g+1), K(g+2) during PV(g).
     template <bool MORE, bool MASKN, bool ROWMASK = false>
-    __device__ __forceinline__ void block(const u16 *__restrict__ vsp, int vsb, const u16 *__restrict__ ksp0,
-                                          const u16 *__restrict__ ksp1, int ksb, const u32x4 (&qf)[KS],
-                                          const u32x4 &zpat, int lo, int hi, int hf, float c, bool keep = true) {
-        constexpr int NA = MORE ? KS : 1;  // slices of the QK half
-        constexpr int NV = 2 * DT;         // V fragments, read in the first NAV slices
-        constexpr int NAV = NA > 1 ? NA / 2 : 1;
-        constexpr int NB = 2 * DT + 2;     // slices of the PV half
-        constexpr int NBK = KS > 1 ? KS / 2 : 1;  // slices that read K(g+2)
-        f32x16 sn;
-        u32x4 pb[2];
-        __builtin_amdgcn_sched_barrier(0);
-        // ---- QK(g+1) || V(g) reads, exponentials and packing of step g
+    __device__ __forceinline__ void block(const u16 *__restrict__ vs, int vbase, const u16 *__restrict__ ks,
+                                          int kbase, const u32x4 (&qf)[NB][KS], const LdsOfs &of, int lo,
+                                          int hi, int g4, float c, unsigned keep = ~0u) {
+        const u32x4 ones = {O::ONE2, O::ONE2, O::ONE2, O::ONE2};
+        f32x4 sn[NB][2];
+        if (MORE) TM::qk(kf, qf, sn);
+        TM::load_v(vs, of, vbase, vf);
+        u32x4 pb[NB];
 #pragma unroll
-        for (int i = 0; i < NA; ++i) {
-            if (MORE) {
-                if (i == 0) {
+        for (int nb = 0; nb < NB; ++nb) {
+            float pr[8];
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) sn[e] = 0.f;
-                }
-                sn = mma32(kf[i], qf[i], sn);
-            }
-            constexpr int VPS = (NV + NAV - 1) / NAV, XPS = 16 / NA;  // V fragments, exponentials per slice
-#pragma unroll
-            for (int v2 = 0; v2 < VPS; ++v2) {
-                const int v = i * VPS + v2;
-                if (i < NAV && v < NV)
-                    vf[v] = tr_pair(vsp + T::vdelta(vsb, v & 1, 0, v >> 1), vsp + T::vdelta(vsb, v & 1, 1, v >> 1));
-            }
-#pragma unroll
-            for (int e2 = 0; e2 < XPS; e2 += 2) {
-                const int e = i * XPS + e2;
-                pb[e >> 3][(e & 7) >> 1] = Ops<FP16>::pack(fast_exp2(s[e]), fast_exp2(s[e + 1]));
-            }
-            __builtin_amdgcn_sched_barrier(0);
+            for (int i = 0; i < 8; ++i) pr[i] = fast_exp2(__builtin_fmaf(s[nb][i >> 2][i & 3], c, -m[nb]));
+            pb[nb] = u32x4{O::pack(pr[0], pr[1]), O::pack(pr[2], pr[3]), O::pack(pr[4], pr[5]),
+                           O::pack(pr[6], pr[7])};
+            if (ROWMASK && !((keep >> nb) & 1)) pb[nb] = u32x4{0u, 0u, 0u, 0u};
         }
-        if (ROWMASK && !keep) pb[0] = pb[1] = u32x4{0u, 0u, 0u, 0u};
-        // ---- PV(g) + denominator || K(g+2) reads, masking, maxima and c*s - m of step g+1
-        constexpr int NE = MORE ? (16 + NB - 2) / (NB - 1) : 0;  // score elements per slice after the first
-        float mx = 0.f;
+        if (MORE) {
+            // 2*KS*NB QK MFMAs; the V reads go out with the first half of them
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            if (j < 2 * DT)
-                o[j >> 1] = mma32(vf[j], pb[j & 1], o[j >> 1]);  // d tile j/2, tokens 16 (j&1) ..
-            else
-                z = Ops<FP16>::mma_k32(zpat, pb[j - 2 * DT], z);
-            if (MORE) {
-                constexpr int KPS = (KS + NBK - 1) / NBK;  // K fragments per slice
-#pragma unroll
-                for (int k2 = 0; k2 < KPS; ++k2) {
-                    const int k = j * KPS + k2;
-                    if (j < NBK && k < KS) {
-                        const int e = 2 * T::BLK * k + 8 * ksb;
-                        kf[k] = tr_pair(ksp0 + e, ksp1 + e);
-                    }
-                }
-                if (j == 1 && MASKN) {
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const int tok = 8 * (e >> 2) + 4 * hf + (e & 3);
-                        if (tok < lo || tok >= hi) sn[e] = NEG_INF;
-                    }
-                }
-                if (j >= 1) {
-#pragma unroll
-                    for (int e2 = 0; e2 < NE; ++e2) {
-                        const int e = (j - 1) * NE + e2;
-                        if (e < 16) {
-                            mx = e == 0 ? sn[0] : fmaxf(mx, sn[e & 15]);
-                            s[e & 15] = __builtin_fmaf(sn[e & 15], c, -m);
-                        }
-                    }
-                    // keeps this slice's maxima in the slice (instruction
-                    // selection otherwise gathers the chain after the last MFMA)
-                    if ((j - 1) * NE < 16) asm volatile("" : "+v"(mx));
-                }
+            for (int i = 0; i < 2 * KS * NB; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                if (i < DB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+                __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);  // transcendental
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
-        if (MORE) lm = ROWMASK && !keep ? NEG_INF : mx;
-    }
-
-    // One staged tile of an attached segment (after the pipeline has
-    // drained): tokens [lo, hi) of the tile, for this lane's row only if
-    // keep.  Rows not kept get P = 0 and keep their running maxima.  The
-    // tile's two steps run as a two-step pipeline (the QK of the second step
-    // beside the exponentials and PV of the first).
-    __device__ void tail_tile(const u16 *__restrict__ st, const u32x4 (&qf)[KS], const Lane32 &lc,
-                              const u32x4 &zpat, int lo, int hi, bool keep, int hf, float c, float rc) {
-        load_k(st, lc, 0, kf);
-        f32x16 sn = qk(kf, qf);
-        mask_max<true>(sn, lo, hi, hf);
-        if (!keep) lm = NEG_INF;
-        rescale<false>(c, rc);
-        shift(sn, c);
-        if (hi > 32) {
-            load_k(st, lc, 32, kf);
-            // the K read-ahead of this block has no step to read: it rereads step 0
-            block<true, true, true>(st + lc.vof, 0, st + lc.kof0, st + lc.kof1, 0, qf, zpat, lo - 32, hi - 32, hf, c,
-                                    keep);
-            rescale<true>(c, rc);
-            block<false, false, true>(st + lc.vof, 32, st, st, 0, qf, zpat, 0, 32, hf, c, keep);
-        } else {
-            block<false, false, true>(st + lc.vof, 0, st, st, 0, qf, zpat, 0, 32, hf, c, keep);
+        __builtin_amdgcn_sched_barrier(0);  // K(g+1) is dead only after QK(g+1)
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) o[nb][db] = O::mma_k32(vf[db], pb[nb], o[nb][db]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) z[nb] = O::mma_k32(ones, pb[nb], z[nb]);
+        if (MORE) {
+            TM::load_k(ks, of, kbase, kf);
+            finish_scores<MASKN>(sn, lo, hi, g4);
+        }
+        // instruction order: QK MFMAs alternate with the exponentials and the
+        // V reads, then PV MFMAs alternate with the K reads and the score epilogue
+        if (MORE) {
+            // DB*NB PV MFMAs; the K reads go out with the first half of them
+#pragma unroll
+            for (int i = 0; i < DB * NB; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+                if (i < 2 * KS) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);  // VALU
+            }
         }
     }
 
-    // Store the wave's 32 partial rows (rows row0 + r, r < 32, those below
-    // nrows) through the wave's 8 KiB LDS region `stg`, so that every store
-    // instruction writes whole 64-byte lines (straight from the registers a
-    // row's 256 bytes sit in two lanes, and the nontemporal write path did
-    // not combine the two halves of a line written by two instructions).
-    // Same format as store_partial: (o / z) 2^-e in fp16 at part_pos order,
-    // then (log-sum-exp, e).  In the region, 16-byte chunk c of row r sits at
-    // chunk c ^ (r % (D / 8)): the 16 rows a write instruction touches hit
-    // distinct banks without padding.
-    __device__ void store(u16 *__restrict__ stg, u16 *__restrict__ part, float *__restrict__ lse2,
-                          const int32_t *__restrict__ rowbase_job, int row0, int nrows, int hq, int hcol, int group,
-                          int lane) {
-        constexpr int CPR = D / 8;        // 16-byte chunks per row
-        constexpr int RPI = 64 / CPR;     // rows per store instruction
-        const int r = lane & 31, hf = lane >> 5;
-        const float za = __shfl(z[0], lane & 15), zb = __shfl(z[1], lane & 15);
-        const float zr = (lane & 16) ? zb : za;
-        const bool any = m != NEG_INF;
-        const float inv = any ? 1.f / zr : 0.f;
-        float amax = 0.f;
+    // One staged tile of an attached private segment (after the pipeline has
+    // drained): tokens [lo, hi) of the tile, for this wave's rows [rlo, rhi)
+    // only.  Other rows get P = 0 and keep their running maxima, so their
+    // state is unchanged.
+    __device__ void tail_tile(const u16 *__restrict__ st, const u32x4 (&qf)[NB][KS], const LdsOfs &of, int lo,
+                              int hi, int rlo, int rhi, int row, int g4, float c, float rc) {
+        unsigned keep = 0;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+        for (int nb = 0; nb < NB; ++nb) keep |= (unsigned)(16 * nb + row >= rlo && 16 * nb + row < rhi) << nb;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) amax = fmaxf(amax, __builtin_fabsf(o[dt][e]));
-        amax *= inv;
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
-        const int ex = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
-        const float sc = __builtin_amdgcn_ldexpf(inv, -ex);
-        // lane (r, hf) holds d = 32 dt + 8 q + 4 hf + i in o[dt][4 q + i]; at
-        // part_pos order q = 0 and 2 fill chunk 4 dt + hf, q = 1 and 3 chunk
-        // 4 dt + 2 + hf
-        u16 *srow = stg + r * D;
-        const int sw = r % CPR;
+        for (int k = 0; k < T::TT / 32; ++k) {
+            const int base = 32 * k;
+            if (base >= hi) break;
+            f32x4 sn[NB][2];
+            TM::load_k(st, of, base, kf);
+            TM::qk(kf, qf, sn);
+            finish_scores<true>(sn, lo - base, hi - base, g4);
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            const f32x16 a = o[dt] * sc;
-            const u32x4 w0 = {pack_f16(a[0], a[1]), pack_f16(a[2], a[3]), pack_f16(a[8], a[9]),
-                              pack_f16(a[10], a[11])};
-            const u32x4 w1 = {pack_f16(a[4], a[5]), pack_f16(a[6], a[7]), pack_f16(a[12], a[13]),
-                              pack_f16(a[14], a[15])};
-            *(u32x4 *)(srow + 8 * ((4 * dt + hf) ^ sw)) = w0;
-            *(u32x4 *)(srow + 8 * ((4 * dt + 2 + hf) ^ sw)) = w1;
-        }
-        const float l = any ? (m + __builtin_amdgcn_logf(zr)) * LN2 : NEG_INF;
-        const int grow = row0 + r;
-        if (hf == 0 && grow < nrows) {
-            const int lr = grow / group;
-            const size_t prow = (size_t)(rowbase_job[0] + lr) * hq + hcol + (grow - lr * group);
-            __builtin_nontemporal_store(f32x2{l, (float)ex}, (f32x2 *)(lse2 + 2 * prow));
-        }
-        // the wave reads back its own rows only
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-        __builtin_amdgcn_wave_barrier();
-        const int ck = lane % CPR;
-#pragma unroll
-        for (int k = 0; k < 32 / RPI; ++k) {
-            const int rr = RPI * k + lane / CPR;
-            const u32x4 w = *(const u32x4 *)(stg + rr * D + 8 * (ck ^ (rr % CPR)));
-            const int gr = row0 + rr;
-            if (gr < nrows) {
-                const int lr = gr / group;
-                const size_t prow = (size_t)(rowbase_job[0] + lr) * hq + hcol + (gr - lr * group);
-                __builtin_nontemporal_store(w, (u32x4 *)(part + prow * D + 8 * ck));
-            }
+            for (int nb = 0; nb < NB; ++nb)
+                if (!((keep >> nb) & 1)) lm[nb] = NEG_INF;
+            rescale(c, rc);
+            block<false, false, true>(st, base, st, 0, qf, of, 0, 32, g4, c, keep);
         }
     }
 };
@@ -869,37 +606,35 @@ struct Pipe32 {
 #ifndef TA_PIPE_PRO
 #define TA_PIPE_PRO 3  // measured: 3 of 5 tiles in the prologue start the loop earliest
 #endif
-#ifndef TA_PIPE_SYNC
-#define TA_PIPE_SYNC 1
-#endif
 
+// STAGES LDS tiles; the waves meet at a barrier every SYNC tiles.  While the
+// waves work on tiles t .. t+SYNC-1 they read those and the K of tile t+SYNC
+// (the pipelined steps read one step ahead), so SYNC+1 tiles are resident
+// and STAGES-SYNC-1 more can be in flight.  The prologue issues PRO tiles;
+// the first loop barrier issues the rest of the ring.
 // One 256-row work item of the pipelined kernel, with its attached segments
-// (p.xtail, indexed by the item), STAGES LDS stages at `lds`.  STAGES LDS
-// tiles; the waves meet at a barrier every SYNC tiles.  While the waves work
-// on tiles t .. t+SYNC-1 they read those and the K of tile t+SYNC (the
-// pipelined steps read one step ahead), so SYNC+1 tiles are resident and
-// STAGES-SYNC-1 more can be in flight.  The prologue issues PRO tiles; the
-// first loop barrier issues the rest of the ring.
-template <int D, bool FP16, int NW, int STAGES = TA_PIPE_STAGES, int PRO = TA_PIPE_PRO, int SYNC = TA_PIPE_SYNC>
+// (p.xtail, indexed by the item), STAGES LDS stages at `lds`.
+template <int D, bool FP16, int NW, int NB = 2, int STAGES = TA_PIPE_STAGES, int SYNC = 1, int PRO = TA_PIPE_PRO>
 __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__restrict__ items, int item, u16 *lds,
                                           int tid) {
-    using T = Tile32<D>;
-    using M = Pipe32<D, FP16>;
+    using T = Tile<D>;
+    using M = PipeMath<D, FP16, NW, NB>;
+    using TM = TileMath<D, FP16, NB, NW>;
     constexpr int KS = M::KS;
     constexpr int BPW = T::NBLK / NW;  // copies per wave per tile
-    static_assert(NW == 8, "eight 32-row waves");
+    static_assert(T::NBLK % NW == 0, "every wave copies the same number of blocks");
     static_assert(SYNC >= 1 && STAGES >= 2 * SYNC + 1 && STAGES <= 5,
                   "a group's tiles, the next K and the next group's copies fit the stages");
     static_assert(PRO >= SYNC + 1 && PRO <= STAGES, "the prologue issues the tiles the first group reads");
     const int job = items[3 * item], row0 = items[3 * item + 1], h = items[3 * item + 2];
 
     const int lane = tid & 63, wave = tid >> 6;
-    const int hf = lane >> 5;
+    const int row = lane & 15, g4 = lane >> 4;
     const int kst = p.kstart[job];
     const int ntok = max(0, min(p.klen[job], p.tcap - kst));
     const int kend = kst + ntok;
     const int nrows = p.qlen[job] * p.group;
-    const int wrow0 = row0 + 32 * wave;
+    const int wrow0 = row0 + 16 * NB * wave;
     const bool active = wrow0 < nrows;
     const float c = p.scale_log2, rc = 1.f / p.scale_log2;
     const int tb0 = kst & ~7;
@@ -907,14 +642,13 @@ __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__r
     const int nsteps = ntok > 0 ? (kend - tb0 + 31) / 32 : 0;
     auto tile_stage = [&](int t) { return lds + (t % STAGES) * T::ELEMS; };
     auto stage = [&](int g) { return tile_stage(g >> 1); };  // stage of step g's tile
-    const Lane32 lc = M::lane_consts(lane, p.tcap);
 
     // Attached segments (xtail record of this item: count, then (first token,
-    // tokens, first job row, rows) for up to TA_XTAIL_MAX segments) follow
-    // the job's own tiles in one tile sequence through the same LDS stages.
-    // The record is read at once (constant address space: one batch of scalar
-    // loads, no chain of dependent loads) into per-segment values that
-    // unrolled loops index with constants.
+    // tokens, first job row, rows) for up to TA_XTAIL_MAX segments)
+    // follow the job's own tiles in one tile sequence through the same LDS
+    // stages.  The record is read at once (constant address space: one batch
+    // of scalar loads, no chain of dependent loads) into per-segment values
+    // that unrolled loops index with constants.
     constexpr int XM = TA_XTAIL_MAX;
     constexpr int XF = 4;  // fields per segment
     int rec[1 + XF * XM];
@@ -941,7 +675,7 @@ __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__r
     // copy tile t of the sequence into stage st
     auto copy_tile = [&](int t, u16 *st) {
         if (t < ntiles) {
-            M::template copy<NW>(st, p.kp, p.vp, h, p.tcap, tb0 + t * T::TT, kst, kend, wave, lane, lc);
+            TM::copy(st, p.kp, p.vp, h, p.tcap, tb0 + t * T::TT, kst, kend, wave, lane);
             return;
         }
         int t0n = 0, cs = 0, ce = 1;
@@ -952,7 +686,7 @@ __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__r
                 cs = xs[k];
                 ce = xe[k];
             }
-        M::template copy<NW>(st, p.kp, p.vp, h, p.tcap, t0n, cs, ce, wave, lane, lc);
+        TM::copy(st, p.kp, p.vp, h, p.tcap, t0n, cs, ce, wave, lane);
     };
 
     int issued = 0;  // tiles of the sequence whose copies this wave has issued
@@ -968,60 +702,54 @@ __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__r
     // lane loads a valid row (rows past the job are zeroed afterwards); tiles
     // 1 .. PRO-1 follow.
     const int qb = p.qbase ? p.qbase[job] : -1;
-    const int rr = max(0, min(wrow0 + (lane & 31), nrows - 1));  // this lane's (clamped) query row
+    int rq[NB];
     if (qb < 0 && ntot > 0) copy_tile(0, lds);
-    const int rq = qb >= 0 ? qb + rr / p.group : p.qids[(size_t)job * p.maxr + rr / p.group];
-    // Q^T fragments (B operand): lane l holds row l % 32, d = 16 ks + 8 (l >> 5) .. +7
-    u32x4 qf[KS];
-    {
-        const u16 *src = p.q + ((size_t)rq * p.hq + h * p.group + rr % p.group) * D + 8 * hf;
 #pragma unroll
-        for (int k = 0; k < KS; ++k) qf[k] = *(const u32x4 *)(src + 16 * k);
+    for (int nb = 0; nb < NB; ++nb) {
+        const int rr = max(0, min(wrow0 + 16 * nb + row, nrows - 1));
+        rq[nb] = qb >= 0 ? qb + rr / p.group : p.qids[(size_t)job * p.maxr + rr / p.group];
     }
-#ifdef TA_PIPE_QFIRST
-    __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
-#endif
+    u32x4 qf[NB][KS];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int rr = max(0, min(wrow0 + 16 * nb + row, nrows - 1));
+        const u16 *src = p.q + ((size_t)rq[nb] * p.hq + h * p.group + rr % p.group) * D + 8 * g4;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) qf[nb][k] = *(const u32x4 *)(src + 32 * k);
+    }
     if (qb >= 0 && ntot > 0) copy_tile(0, lds);  // behind the Q loads: one wait covers both
-    {
-        const bool valid = wrow0 + (lane & 31) < nrows;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const bool valid = wrow0 + 16 * nb + row < nrows;
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
-            if (!valid) qf[k] = u32x4{0, 0, 0, 0};
-            asm volatile("" : "+v"(qf[k]));
+            if (!valid) qf[nb][k] = u32x4{0, 0, 0, 0};
+            asm volatile("" : "+v"(qf[nb][k]));
         }
     }
     for (int t = 1; t < PRO && t < ntot; ++t) copy_tile(t, tile_stage(t));
     issued = min(PRO, ntot);
 
-    // denominator MFMA operand: lane l of the 16x16x32 A operand is row
-    // l % 16, k block l / 16; rows 0 and 1 sum the k blocks of 32-row P rows
-    // 0-15 and 16-31
-    u32x4 zpat;
-    {
-        const int zr = lane & 15, kb = (lane >> 4) & 1;
-        const u32 one = (zr == 0 && kb == 0) || (zr == 1 && kb == 1) ? Ops<FP16>::ONE2 : 0u;
-        zpat = u32x4{one, one, one, one};
-    }
-
     M acc;
     acc.reset();
+    const LdsOfs of = T::offsets(row, g4);
 
     wait_tiles<BPW>(issued - 1);  // tile 0 landed (tiles 1 .. PRO-1 may be in flight)
     __builtin_amdgcn_s_barrier();
     if (active && nsteps > 0) {
-        M::load_k(lds, lc, 0, acc.kf);
-        f32x16 s0 = M::qk(acc.kf, qf);
-        acc.template mask_max<true>(s0, kst - tb0, kend - tb0, hf);
-        acc.template rescale<false>(c, rc);
-        acc.shift(s0, c);
-        if (nsteps > 1) M::load_k(lds, lc, 32, acc.kf);
+        f32x4 s0[NB][2];
+        TM::load_k(lds, of, 0, acc.kf);
+        TM::qk(acc.kf, qf, s0);
+        acc.template finish_scores<true>(s0, kst - tb0, kend - tb0, g4);
+        acc.rescale(c, rc);
+        if (nsteps > 1) TM::load_k(lds, of, 32, acc.kf);
     }
 
     // Entering tile t (at step 2t): at the start of a group (t % SYNC == 0)
     // tiles t+1 .. t+SYNC must have landed (the earlier ones were waited for
     // at the previous group); the later issued ones may still be in flight.
-    // Once every wave passed the barrier the stages of the previous group
-    // are free for tiles up to t+STAGES-1.
+    // Once every wave passed the barrier the stages of the previous group are
+    // free for tiles up to t+STAGES-1.
     auto sync_tile = [&](int t) {
         if (t % SYNC != 0 || t + 1 >= ntot) return;
         wait_tiles<BPW>(max(0, issued - 1 - (t + SYNC)));
@@ -1034,95 +762,66 @@ __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__r
         if (!(g & 1)) sync_tile(g >> 1);
         if (active) {
             const int gk = g + 2;
-            acc.template block<true, false>(stage(g) + lc.vof, 32 * (g & 1), stage(gk) + lc.kof0,
-                                            stage(gk) + lc.kof1, 32 * (gk & 1), qf, zpat, 0, 32, hf, c);
-            acc.template rescale<true>(c, rc);
+            acc.template block<true, false>(stage(g), 32 * (g & 1), stage(gk), 32 * (gk & 1), qf, of, 0, 32,
+                                            g4, c);
+            acc.rescale(c, rc);
         }
     }
     // the last two steps: the successor of step nsteps-2 may be masked at its end
     if (g + 1 < nsteps) {
         if (!(g & 1)) sync_tile(g >> 1);
         if (active) {  // one (masked) form for either end of the job keeps the register allocation simple
-            acc.template block<true, true>(stage(g) + lc.vof, 32 * (g & 1), stage(g + 1) + lc.kof0,
-                                           stage(g + 1) + lc.kof1, 32 * ((g + 1) & 1), qf, zpat, 0,
-                                           kend - (tb0 + 32 * (g + 1)), hf, c);
-            acc.template rescale<true>(c, rc);
+            acc.template block<true, true>(stage(g), 32 * (g & 1), stage(g + 1), 32 * ((g + 1) & 1), qf, of,
+                                           0, kend - (tb0 + 32 * (g + 1)), g4, c);
+            acc.rescale(c, rc);
         }
         ++g;
     }
     if (g < nsteps) {
         if (!(g & 1)) sync_tile(g >> 1);
-        if (active)
-            acc.template block<false, false>(stage(g) + lc.vof, 32 * (g & 1), stage(g), stage(g), 0, qf, zpat, 0, 32,
-                                             hf, c);
+        if (active) acc.template block<false, false>(stage(g), 32 * (g & 1), stage(g), 0, qf, of, 0, 32, g4, c);
     }
 
     // Attached segments, in rounds of up to STAGES tiles that are resident
     // together: one wait and one barrier per round, then every wave attends
     // the round's tiles of the segments holding its rows, side by side.  The
     // root loop (or the prologue) already issued the first tiles.
-    for (int r0 = ntiles; r0 < ntot; r0 += STAGES) {
-        const int r1 = min(r0 + STAGES, ntot);
-        __builtin_amdgcn_s_barrier();  // every wave is done with the tiles before r0
-        for (; issued < r1; ++issued) copy_tile(issued, tile_stage(issued));
-        __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
-        __builtin_amdgcn_s_barrier();  // the round's tiles landed
+    {
+        for (int r0 = ntiles; r0 < ntot; r0 += STAGES) {
+            const int r1 = min(r0 + STAGES, ntot);
+            __builtin_amdgcn_s_barrier();  // every wave is done with the tiles before r0
+            for (; issued < r1; ++issued) copy_tile(issued, tile_stage(issued));
+            __builtin_amdgcn_s_waitcnt(TA_VMCNT(0));
+            __builtin_amdgcn_s_barrier();  // the round's tiles landed
 #pragma unroll
-        for (int k = 0; k < XM; ++k) {
-            const int rlo = rec[3 + XF * k] - wrow0;  // segment rows in this wave: [rlo, rlo + rows)
-            if (xn[k] > 0 && active && rlo >= 0 && rlo < 32) {
-                const int lr = lane & 31;
-                const bool keep = lr >= rlo && lr < rlo + rec[4 + XF * k];
-                for (int i = max(0, r0 - xfirst[k]); i < xn[k] && xfirst[k] + i < r1; ++i) {
-                    const int t0 = (xs[k] & ~7) + i * T::TT;
-                    acc.tail_tile(tile_stage(xfirst[k] + i), qf, lc, zpat, max(0, xs[k] - t0),
-                                  min(T::TT, xe[k] - t0), keep, hf, c, rc);
+            for (int k = 0; k < XM; ++k) {
+                const int rlo = rec[3 + XF * k] - wrow0;  // segment rows in this wave: [rlo, rlo + rows)
+                if (xn[k] > 0 && active && rlo >= 0 && rlo < 16 * NB) {
+                    for (int i = max(0, r0 - xfirst[k]); i < xn[k] && xfirst[k] + i < r1; ++i) {
+                        const int t0 = (xs[k] & ~7) + i * T::TT;
+                        acc.tail_tile(tile_stage(xfirst[k] + i), qf, of, max(0, xs[k] - t0), min(T::TT, xe[k] - t0),
+                                      rlo, rlo + rec[4 + XF * k], row, g4, c, rc);
+                    }
                 }
             }
         }
     }
 
-    // Partial rows through LDS.  When the item's attached tiles fit one
-    // round with a stage to spare (the stage of its last own tile, which
-    // every wave finished before the round) and at most four waves hold no
-    // attached rows, those waves stage their rows there (8 KiB each) and the
-    // waves with attached rows in the stage of their own last attached tile
-    // (no other wave reads it), so no wave waits for another.  Otherwise the
-    // waves meet at a barrier and stage at wave * 8 KiB.
-    const int nxt = ntot - ntiles;
-    int owners = 0;  // waves that hold rows of an attached segment
-#pragma unroll
-    for (int k = 0; k < XM; ++k) {
-        const int ow = (rec[3 + XF * k] - row0) >> 5;
-        if (xn[k] > 0 && ow >= 0 && ow < 8) owners |= 1 << ow;
-    }
-    const int free_waves = 8 - __builtin_popcount(owners);
-    const bool spare = ntiles > 0 && nxt > 0 && nxt < STAGES && free_waves <= 4;
-    u16 *stg;
-    if (spare) {
-        if ((owners >> wave) & 1) {
-            int last = 0;  // this wave's last attached tile
-#pragma unroll
-            for (int k = 0; k < XM; ++k)
-                if (xn[k] > 0 && ((rec[3 + XF * k] - row0) >> 5) == wave) last = max(last, xfirst[k] + xn[k] - 1);
-            stg = tile_stage(last);
-        } else {
-            const int rank = __builtin_popcount(~owners & ((1 << wave) - 1));  // free waves before this one
-            stg = tile_stage(ntiles - 1) + rank * 32 * D;
-        }
-    } else {
-        __builtin_amdgcn_s_barrier();
-        stg = lds + wave * 32 * D;
-    }
     if (!active) return;
-    acc.store(stg, p.part, p.lse, p.rowbase + job, wrow0, nrows, p.hq, h * p.group, p.group, lane);
+    const int rb = p.rowbase[job];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int grow = wrow0 + 16 * nb + row;
+        if (grow >= nrows) continue;
+        const int lr = grow / p.group, gg = grow - lr * p.group;
+        const size_t prow = (size_t)(rb + lr) * p.hq + h * p.group + gg;
+        store_partial<M::DB>(p.part, p.lse, prow, acc.o[nb], acc.m[nb], acc.z[nb][0], g4);
+    }
 }
 
 template <int D, bool FP16, int NW>
 __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
-    __shared__ __attribute__((aligned(16))) u16 lds[TA_PIPE_STAGES * Tile32<D>::ELEMS];
-    static_assert(8 * 32 * D <= TA_PIPE_STAGES * Tile32<D>::ELEMS && 4 * 32 * D <= Tile32<D>::ELEMS,
-                  "the partial rows fit the stages, four waves' rows one stage");
+    __shared__ __attribute__((aligned(16))) u16 lds[TA_PIPE_STAGES * Tile<D>::ELEMS];
     pipe_item<D, FP16, NW>(p, p.items, xcd_item(blockIdx.x, gridDim.x), lds, threadIdx.x);
 }
 
