@@ -19,7 +19,10 @@ replay is slightly slower than back-to-back eager launches.  Per-kernel
 every launch through hipExtLaunchKernel events); ``kernel_graph_slot_us`` is
 each kernel's share of a graph of back-to-back launches, gaps included.  The
 roofline figure divides the dominant kernel's algorithmic work by its
-``kernel_us``.
+``kernel_us``; ``roofline.stream_frac`` divides that rate by the box's read
+ceiling, measured in the same run by the library's read-only stream over
+1 GiB (``ta_read_stream``), and ``layer_stream_frac`` does the same for the
+whole layer.
 
 The parity gate comes first: the GPU output must be within 0.3% relative L2
 of the FP32 oracle's per-request attention (oracle/attention_oracle.py, the
@@ -50,6 +53,7 @@ R, HQ, HK, D = 128, 32, 8, 128
 SHARED, PRIVATE = 8128, 64
 POOLS = 8
 REL_L2_BOUND = 3e-3
+STREAM_BLOCKS = 16384  # workgroups of the read-ceiling stream (the fastest of 1024 / 4096 / 16384 measured)
 
 
 def parse():
@@ -201,6 +205,23 @@ def main():
         kernel_slot_us[name] = time_steps(lambda i: kg.replay(), max(1, args.steps // POOLS),
                                           max(1, args.warmup // POOLS)) / POOLS
 
+    # the box's read ceiling in the same run: the library's read-only stream over 1 GiB
+    # (ta_read_stream, 16,384 workgroups), the kernel's own duration from dispatch stamps
+    lib = _native.load()
+    stream_bytes = 1 << 30
+    src = torch.ones(stream_bytes, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(4 * STREAM_BLOCKS, dtype=torch.int32, device=dev)
+
+    def read_stream(i):
+        _native.check(lib.ta_read_stream(src.data_ptr(), stream_bytes, sink.data_ptr(), STREAM_BLOCKS,
+                                         stream.cuda_stream))
+
+    for i in range(3):
+        read_stream(i)
+    stream_us = statistics.median(launch_durations_us(read_stream, 10))
+    stream_gbs = stream_bytes / (stream_us * 1e-6) / 1e9
+    del src, sink
+
     # per-request execution through the same kernels (the "faster than per-request" check)
     req_prepared = prepare(schedule(tree, HQ, HK, D, "request", model), qd)
     per_request_us = time_steps(lambda i: attention_matrix(qd, *pools[i % POOLS], req_prepared),
@@ -254,7 +275,11 @@ def main():
     roofline = {"kernel": dominant, "bound": bound, "achieved": main["achieved"], "peak": main["peak"],
                 "unit": main["unit"], "frac": main["frac"], "traffic": traffic, "kernel_us": round(kernel_us[dominant], 3),
                 "floor_us": main["floor_us"], "algorithmic": work,
-                ("mfma" if bound == "hbm" else "hbm"): other}
+                ("mfma" if bound == "hbm" else "hbm"): other,
+                # against the box's measured read ceiling instead of the 8 TB/s peak
+                "stream_gbs": round(stream_gbs, 1), "stream_frac": round(hbm["achieved"] / stream_gbs, 4),
+                "stream": f"ta_read_stream over {stream_bytes} B, {STREAM_BLOCKS} workgroups, median of 10 "
+                          f"dispatch-stamped launches: {stream_us:.1f} us"}
 
     kv_bytes = physical_kv_bytes(T)
     value = kv_bytes / (us_per_layer * 1e-6) / 1e9
@@ -270,6 +295,7 @@ def main():
                    "method": args.method, "cost_model": args.cost_model, "kv_pools": POOLS,
                    "timing": "eager", "physical_kv_bytes": kv_bytes},
         "layer_hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "layer_stream_frac": round(value / stream_gbs, 4),
         "graph_us_per_layer": round(graph_us, 3),
         "per_request_us_per_layer": round(per_request_us, 3),
         "speedup_vs_per_request": round(per_request_us / us_per_layer, 3),

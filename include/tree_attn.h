@@ -78,7 +78,8 @@ typedef struct ta_plan {
     const int32_t *qids;      /* [njobs * maxr]                                   */
     const int32_t *kstart;    /* [njobs] first physical token of each job          */
     const int32_t *qlen;      /* [njobs] requests per job                          */
-    const int32_t *klen;      /* [njobs] tokens per job (device-updatable)         */
+    const int32_t *klen;      /* [njobs] tokens per job (device-updatable; attached
+                               * tails keep theirs in xtail, see below)           */
     const int32_t *rowbase;   /* [njobs] first partial slot of each job            */
     const int32_t *slots;     /* [nreq * maxs] partial slots of each request       */
     const int32_t *counts;    /* [nreq] number of slots of each request            */
@@ -101,7 +102,13 @@ typedef struct ta_plan {
      * one wave (32 rows): a private tail (the group rows of one request) or a
      * node of a few consecutive requests.  The item folds the tokens into those
      * rows' partials, so the segment has no partial slot of its own.  Needs
-     * tcap % 8 == 0 (ta_attention_matrix returns TA_ERR_ARG otherwise). */
+     * tcap % 8 == 0 (ta_attention_matrix returns TA_ERR_ARG otherwise).
+     * Decode steps: a growing tail's length lives in klen[j] when the tail is
+     * job j, and in the tokens field (int 2 + 4k of the item's record) of
+     * every record that holds it as segment k when it is attached; a caller
+     * that lengthens its tails between steps rewrites all of these positions
+     * (kernels.PreparedPlan.grow_offsets lists them within the plan's
+     * metadata buffer), not klen alone. */
     const int32_t *xtail;
     int32_t xtail_stride;
     /* [njobs] or NULL: the first request id of each job whose requests are

@@ -74,6 +74,23 @@ def test_xtail_record_layout_matches_header():
     assert kernels.XTAIL_FIELDS == 4
 
 
+def test_python_constants_match_header():
+    """Every constant _native mirrors equals its #define in include/tree_attn.h."""
+    header = HEADER.read_text()
+
+    def define(name):
+        m = re.search(rf"#define {name} \(?(\d+)u?(?: << (\d+))?\)?", header)
+        assert m, name
+        return int(m.group(1)) << int(m.group(2) or 0)
+
+    assert define("TA_NOALLOC_SCRATCH_BYTES") == _native.NOALLOC_SCRATCH_BYTES == 32 << 20
+    assert define("TA_ERR_SCRATCH") == _native.TA_ERR_SCRATCH
+    assert define("TA_ERR_ARG") == _native.TA_ERR_ARG
+    for name in ("TA_BF16", "TA_FP16", "TA_SMALL", "TA_LARGE64", "TA_LARGE128", "TA_LARGE256", "TA_TAIL",
+                 "TA_NKINDS"):
+        assert define(name) == getattr(_native, name), name
+
+
 def test_decode_append_rejects_host_slots_outside_the_pool():
     """Slots given as host data are range-checked before any launch (the eager
     index_copy_ of the reference adapter, qwen.py:89-90, raises for them too)."""

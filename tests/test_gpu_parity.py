@@ -217,7 +217,10 @@ def test_large_row_tiles_all_kinds(pad, dtype, device):
 
 @pytest.mark.parametrize("name", ["deep", "wide"])
 def test_attention_packs_and_c_abi_phases_agree(name, device):
-    """attention(q,k,v) == attention_matrix on packed pools == explicit ta_segment + ta_merge calls."""
+    """attention(q,k,v) == attention_matrix on packed pools == per-kind launches of the plan
+    (kernels.segment / kernels.merge, i.e. ta_segment_plan + ta_merge_plan) and the fused
+    tail-merge order (kernels.tail_merge).  The raw ta_segment / ta_merge entry points are
+    covered by test_raw_segment_and_merge_entry_points."""
     tree = shapes.tree(shapes.benchmark_cases()[name])
     q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 3)
     qd, kd, vd = q.to(device), k.to(device), v.to(device)
@@ -243,6 +246,51 @@ def test_attention_packs_and_c_abi_phases_agree(name, device):
         assert torch.equal(b, d)
     # the unfused order merges in another order: equal up to rounding
     assert relative_l2(b.cpu(), c.cpu().float()) < 5e-4
+
+
+@pytest.mark.parametrize("name,dtype,pad", [("deep", torch.bfloat16, 0), ("wide", torch.float16, 0),
+                                            ("unequal", torch.bfloat16, 3)])
+def test_raw_segment_and_merge_entry_points(name, dtype, pad, device):
+    """The raw C-ABI entry points as a C or ctypes caller of the reference's _segment and
+    _merge (kernels.py:8-83, launched at :158-167) binds them: ta_segment once per work-item
+    kind with plain device pointers and sizes from a prepared plan, then ta_merge over every
+    request's slot list, against the FP32 oracle.  No attachments (ta_segment takes no
+    attachment records); pad 3 gives a pool capacity that is not a multiple of 8."""
+    tree = shapes.tree(shapes.benchmark_cases()[name])
+    q, k, v = make_inputs(tree, 32, 8, 128, dtype, 17, tcap=tree.storage_tokens + pad)
+    ref = oracle_fp32(q, k, v, tree)
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    prepared = prepare(schedule(tree, method="cube", model=MI355X_LIKE), qd, attach_tails=False)
+    abi = prepared.abi
+    lib = _native.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    tcap = kp.shape[2]
+    prepared.part.zero_()
+    kinds = [kind for kind in range(_native.TA_NKINDS) if abi.n_items[kind]]
+    say("raw", name, dtype, pad, "kinds", kinds)
+    for kind in kinds:
+        _native.check(lib.ta_segment(qd.data_ptr(), kp.data_ptr(), vp.data_ptr(), abi.qids, abi.kstart, abi.qlen,
+                                     abi.klen, abi.rowbase, abi.items[kind], abi.n_items[kind], kind, abi.part,
+                                     abi.lse, abi.nreq, abi.hq, abi.hk, abi.d, tcap, abi.maxr, abi.dtype, stream))
+    out = torch.full_like(qd, float("nan"))
+    _native.check(lib.ta_merge(abi.part, abi.lse, abi.slots, abi.counts, out.data_ptr(), abi.nreq, abi.hq, abi.d,
+                               abi.maxs, abi.dtype, stream))
+    torch.cuda.synchronize()
+    check(out, ref, 0.008, 0.03, f"raw ta_segment + ta_merge {name}")
+    # the plan-level layer merges in another order: equal up to rounding
+    b = attention_matrix(qd, kp, vp, prepared).clone()
+    torch.cuda.synchronize()
+    assert relative_l2(out.cpu().float(), b.cpu().float()) < 5e-4
+    # a plan's work items of one kind cover the job rows once: ta_segment twice gives the same partials
+    if kinds:
+        before = prepared.part.clone()
+        kind = kinds[0]
+        _native.check(lib.ta_segment(qd.data_ptr(), kp.data_ptr(), vp.data_ptr(), abi.qids, abi.kstart, abi.qlen,
+                                     abi.klen, abi.rowbase, abi.items[kind], abi.n_items[kind], kind, abi.part,
+                                     abi.lse, abi.nreq, abi.hq, abi.hk, abi.d, tcap, abi.maxr, abi.dtype, stream))
+        torch.cuda.synchronize()
+        assert torch.equal(prepared.part, before)
 
 
 @pytest.mark.parametrize("hq,hk,d,dtype,pad", [(32, 8, 128, torch.bfloat16, 0), (32, 4, 64, torch.float16, 8),

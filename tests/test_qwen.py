@@ -102,6 +102,34 @@ def test_pool_layout_and_capacity_cpu(monkeypatch):
         cached.step([1, 1, 1, 1])
 
 
+def decoder_state(decoder):
+    return ([list(s) for s in decoder.sequences], list(decoder.tree.paths), decoder.used, decoder.generated)
+
+
+@pytest.mark.parametrize("cached", [False, True])
+def test_refused_step_leaves_the_decoder_unchanged_cpu(cached, monkeypatch):
+    """A step refused for capacity (max_new_tokens spent, or pool slots past the pools'
+    capacity) raises before it appends a token, extends the tree or advances the counters."""
+    model = tiny_model(torch.float32, "cpu")
+    cls = integration.CachedPrefixDecoder if cached else integration.SharedKVDecoder
+    decoder = cls(model, SEQUENCES, 2, "cube")
+    monkeypatch.setattr(integration, "attention_matrix", OracleAttention(decoder))
+    decoder.step([0, 1, 2, 3])
+    before = decoder_state(decoder)
+    # pools shorter than the next step's slots (request 3 writes prefix + 3 * 2 + 1 = 19)
+    full = decoder.pools
+    decoder.pools = [(kp[:, :, :16], vp[:, :16]) for kp, vp in full]
+    with pytest.raises(ValueError, match="pool capacity"):
+        decoder.step([4, 5, 6, 7])
+    assert decoder_state(decoder) == before
+    decoder.pools = full
+    decoder.step([4, 5, 6, 7])
+    before = decoder_state(decoder)
+    with pytest.raises(ValueError, match="max_new_tokens"):
+        decoder.step([0, 0, 0, 0])
+    assert decoder_state(decoder) == before
+
+
 # prompts with duplicates, a prompt that is a prefix of others and nested branches
 TREE_SEQUENCES = SEQUENCES + [[1, 2, 9], [1, 2, 3, 4, 5, 6, 7], [7, 8], [1, 2, 3, 4, 5, 6, 7, 13, 14]]
 

@@ -46,7 +46,11 @@ def _call(name, q, kp, vp, abi, out):
 def test_noalloc_equals_attention_matrix(device):
     layers = [("headline 128 x 8192", shapes.headline(), CostModel.mi355x(), 101),
               ("wide 32 x 2112 (smaller)", shapes.benchmark_cases()["wide"], CostModel(), 7),
-              ("headline again", shapes.headline(), CostModel.mi355x(), 5)]
+              ("headline again", shapes.headline(), CostModel.mi355x(), 5),
+              # more than 16 slots per request, mixed kinds: small + 64-row + tail jobs
+              ("unequal, 24 slots", shapes.benchmark_cases()["unequal"], CostModel(), 11),
+              # 52 slots per request: small + 64-row + 256-row jobs with attached tails
+              ("nested, 52 slots", shapes.nested_unequal(), CostModel.mi355x(), 13)]
     for name, spec, model, seed in layers:
         q, kp, vp, prepared = _layer(spec, model, seed, device)
         abi = prepared.abi
@@ -63,8 +67,13 @@ def test_noalloc_equals_attention_matrix(device):
         torch.cuda.synchronize()
         assert torch.isfinite(b.float()).all(), name
         assert torch.equal(a, b), name
-        if name.startswith("wide"):
+        kinds = [k for k in range(_native.TA_NKINDS) if abi.n_items[k] > 0]
+        if name.startswith(("wide", "unequal")):
             assert abi.n_items[_native.TA_TAIL] > 0  # the fused tail-merge kernel ran on the array too
+        if name.startswith(("unequal", "nested")):
+            assert abi.maxs > 16 and len(kinds) >= 3, (abi.maxs, kinds)
+        if name.startswith("nested"):
+            assert abi.xtail
 
 
 def test_noalloc_rejects_plans_beyond_its_array(device):
@@ -76,3 +85,57 @@ def test_noalloc_rejects_plans_beyond_its_array(device):
     torch.cuda.synchronize()
     assert not out.any()  # nothing was launched
     assert b"TA_NOALLOC_SCRATCH_BYTES" in _native.load().ta_error_string(_native.TA_ERR_SCRATCH)
+
+
+_CAPTURE = """
+import ctypes, sys, torch
+sys.path[:0] = {paths!r}
+from tree_attention import CostModel, _native, shapes
+from test_zz_no_alloc import _layer, _call
+dev = torch.device("cuda:0")
+lib = _native.load()
+q, kp, vp, prepared = _layer(shapes.nested_unequal(), CostModel.mi355x(), 21, dev)
+ref = torch.empty_like(q)
+assert _call("ta_attention_matrix", q, kp, vp, prepared.abi, ref) == 0
+bare = _native.TaPlan.from_buffer_copy(prepared.abi)
+bare.part, bare.lse = None, None
+q2, kp2, vp2, prepared2 = _layer(shapes.benchmark_cases()["unequal"], CostModel(), 22, dev)
+ref2 = torch.empty_like(q2)
+assert _call("ta_attention_matrix", q2, kp2, vp2, prepared2.abi, ref2) == 0
+torch.cuda.synchronize()
+out = torch.full_like(q, float("nan"))
+graph, side = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+print("capture: first ta_attention_matrix_noalloc call of the process", flush=True)
+with torch.cuda.graph(graph, stream=side):
+    rc = _call("ta_attention_matrix_noalloc", q, kp, vp, bare, out)
+assert rc == 0, rc
+for rep in range(4):
+    out.fill_(float("nan"))
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), f"replay {{rep}}"
+    # eager work between replays: another layer through the same array
+    other = torch.full_like(q2, float("nan"))
+    assert _call("ta_attention_matrix_noalloc", q2, kp2, vp2, prepared2.abi, other) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(other, ref2), f"eager {{rep}}"
+    print("replay", rep, "equal", flush=True)
+print("ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_graph_capture(device):
+    """The array's address is looked up on a device's first call; here that call
+    is inside a stream capture (a fresh process, so no earlier call set it up).
+    Every replay equals ta_attention_matrix bit for bit, with eager calls on
+    another layer through the same array between the replays."""
+    import subprocess
+    from pathlib import Path
+    here = Path(__file__).resolve().parent
+    paths = [str(here), str(here.parent / "tree-attention-scheduling_amd")]
+    say("noalloc capture subprocess: nested 52 slots, 4 replays")
+    r = subprocess.run([sys.executable, "-c", _CAPTURE.format(paths=paths)], capture_output=True, text=True,
+                       timeout=110)
+    say(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0
+    assert r.stdout.strip().endswith("ok")

@@ -197,11 +197,19 @@ class SharedKVDecoder:
         return cache
 
     # ------------------------------------------------------------ decoding
+    def _step_slots(self, count):
+        """Pool slots of this step's tokens: one per request, in its reserved tail (qwen.py:53-56).
+        Computes them without changing any state."""
+        return [self.prefix_size + r * self.max_new_tokens + self.generated for r in range(count)]
+
     def _next_positions(self, count):
-        """Pool slots of this step's tokens: one per request, in its reserved tail (qwen.py:53-56)."""
-        slots = [self.prefix_size + r * self.max_new_tokens + self.generated for r in range(count)]
+        slots = self._step_slots(count)
         self.generated += 1
         return slots
+
+    def _check_append(self, count):
+        if self.used + count > self.capacity:
+            raise ValueError("Decode exceeds allocated max_new_tokens")
 
     def _prepare_plan(self):
         plan = schedule(self.tree, self.hq, self.hk, self.dim, self.method, self.cost_model)
@@ -210,8 +218,7 @@ class SharedKVDecoder:
         return prepare(plan, shape_of_q)
 
     def _append(self, token_ids):
-        if self.used + len(token_ids) > self.capacity:
-            raise ValueError("Decode exceeds allocated max_new_tokens")
+        self._check_append(len(token_ids))
         slots = self._next_positions(len(token_ids))
         for seq, tok in zip(self.sequences, token_ids):
             seq.append(tok)
@@ -226,10 +233,13 @@ class SharedKVDecoder:
         if len(token_ids) != len(self.sequences):
             raise ValueError("step needs exactly one token per request")
         rope_pos = torch.tensor([[len(s)] for s in self.sequences], device=self.device)
-        positions = self._append(token_ids)
+        # every check before any state changes: a refused step leaves the decoder as it was
+        self._check_append(len(token_ids))
         cap = self.pools[0][0].shape[2]
-        if not all(0 <= p < cap for p in positions):  # host data: the fused kernel would skip them silently
-            raise ValueError(f"pool slots {positions} outside the pool capacity {cap}")
+        planned = self._step_slots(len(token_ids))
+        if not all(0 <= p < cap for p in planned):  # host data: the fused kernel would skip them silently
+            raise ValueError(f"pool slots {planned} outside the pool capacity {cap}")
+        positions = self._append(token_ids)
         slots = torch.tensor(positions, device=self.device, dtype=torch.int32)
         prepared = self._prepare_plan()
         pools = self.pools
@@ -279,9 +289,12 @@ class CachedPrefixDecoder(SharedKVDecoder):
                                  dtype=model.dtype)
         self.cached_plan = CachedDecodePlan(prompt_plan, shape_of_q, self.prefix_size, max_new_tokens)
 
-    def _append(self, token_ids):
+    def _check_append(self, count):
         if self.generated >= self.max_new_tokens:
             raise ValueError("Decode exceeds allocated max_new_tokens")
+
+    def _append(self, token_ids):
+        self._check_append(len(token_ids))
         slots = self._next_positions(len(token_ids))
         for seq, tok in zip(self.sequences, token_ids):
             seq.append(tok)
