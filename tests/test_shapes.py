@@ -14,6 +14,10 @@ def _evaluation_specs():
     specs += list(shapes.benchmark_cases().values())
     specs += [s for _, s in shapes.reference_grid()]
     specs += [s for _, s in shapes.config_grid()]
+    # decode-step layers: the prompt trees plus their reserved and generated tail lengths
+    for _, t, reserved, generated in shapes.decode_layers():
+        lengths = [len(n.tokens) for n in t.nodes] + [reserved, generated]
+        specs.append(([-1] * len(lengths), lengths, [0] * len(t.paths)))
     return specs
 
 
@@ -23,6 +27,10 @@ def test_calibration_grid_is_disjoint_from_evaluation_shapes():
     for _, spec in shapes.calibration_grid():
         lengths, reqs = _lengths_and_requests(spec)
         cal_len |= lengths
+        cal_req |= reqs
+    for _, spec, reserved, generated in shapes.decode_calibration_grid():
+        lengths, reqs = _lengths_and_requests(spec)
+        cal_len |= lengths | {reserved, generated}
         cal_req |= reqs
     ev_len, ev_req = set(), set()
     for spec in _evaluation_specs():

@@ -26,7 +26,13 @@ decode glue (RoPE, the pool scatters and the Q layout in one launch,
 ``kernels.decode_append``) and with the eager ops of the reference adapter.
 Per step it reports the wall time (device synchronised on both sides) and the
 per-layer attention time (HIP events around each ``attention_matrix`` call),
-and checks that both decoders produced identical logits.  Prints one JSON line.
+and checks that both decoders produced identical logits.  At the steps
+``--check-steps`` (0 and 15 by default) every layer's attention output of the
+fused decoder is checked against an fp32 per-request attention over the same
+pools and context paths (atol .008 / rtol .03, as scripts/model_checks.py:45-57
+does), and the JSON line carries each checked step's per-layer relative L2
+error (max and median over the layers); those steps stay out of the timings.
+Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -39,6 +45,7 @@ import torch
 
 from . import CostModel, shapes
 from . import qwen as integration
+from .harness import check, reference_fp32
 
 
 def _model(layers: int, device):
@@ -63,6 +70,7 @@ def main(argv=None):
     ap.add_argument("--method", default="cube")
     ap.add_argument("--warmup", type=int, default=2, help="decode steps run before the timed ones")
     ap.add_argument("--prefill", default="tree", choices=["tree", "request"], help="prefill of the decoders")
+    ap.add_argument("--check-steps", default="0,15", help="steps whose per-layer attention is checked in fp32")
     args = ap.parse_args(argv)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -98,6 +106,8 @@ def main(argv=None):
 
     original = integration.attention_matrix
     attn_events = []
+    check_steps = {int(x) for x in args.check_steps.split(",") if x.strip()}
+    recorded = []  # (q, out, kp, vp) of every layer of a checked step
 
     def timed_attention(q, kp, vp, prepared):
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -105,24 +115,45 @@ def main(argv=None):
         out = original(q, kp, vp, prepared)
         stop.record()
         attn_events.append((start, stop))
+        if recording:
+            recorded.append((q.clone(), out.clone(), kp, vp))
         return out
+
+    def layer_errors(decoder, step):
+        """Every recorded layer against fp32 attention along the prompt paths plus the tails so far."""
+        tails = [[decoder.prefix_size + r * decoder.max_new_tokens + t for t in range(decoder.generated)]
+                 for r in range(len(decoder.sequences))]
+        context = type("Context", (), {"paths": [list(p) + t for p, t in zip(decoder.tree.paths, tails)]})
+        rel = []
+        for layer, (q, out, kp, vp) in enumerate(recorded):
+            ref = reference_fp32(q, kp.permute(2, 0, 1), vp.permute(1, 0, 2), context)
+            rel.append(check(out, ref, f"step {step} layer {layer} attention")["rel_l2"])
+        recorded.clear()
+        return {"layers": len(rel), "context_tokens": len(context.paths[0]), "max": round(max(rel), 6),
+                "median": round(statistics.median(rel), 6), "per_layer": [round(x, 6) for x in rel]}
 
     step_ms = {name: [] for name in decoders}
     attn_us = {name: [] for name in decoders}
     identical = True
+    recording = False
+    layer_rel_l2 = {}
     integration.attention_matrix = timed_attention
     try:
         for step in range(budget):
             tokens = decoders["fused"].logits.argmax(-1).tolist()
             logits = {}
             for name, decoder in decoders.items():
+                recording = name == "fused" and step in check_steps
                 attn_events.clear()
                 torch.cuda.synchronize()
                 t0 = time.perf_counter()
                 logits[name] = decoder.step(tokens)
                 torch.cuda.synchronize()
                 dt = (time.perf_counter() - t0) * 1e3
-                if step >= args.warmup:
+                if recording:
+                    recording = False
+                    layer_rel_l2[step] = layer_errors(decoder, step)
+                elif step >= args.warmup and step not in check_steps:
                     step_ms[name].append(dt)
                     attn_us[name].append(statistics.mean(a.elapsed_time(b) * 1e3 for a, b in attn_events))
             identical &= bool(torch.equal(logits["fused"], logits["eager"]))
@@ -141,6 +172,8 @@ def main(argv=None):
         "glue_saving_us_per_layer": round((statistics.median(step_ms["eager"]) - statistics.median(step_ms["fused"]))
                                           * 1e3 / args.layers, 2),
         "fused_equals_eager": identical,
+        "timed_steps": len(step_ms["fused"]),
+        "attention_rel_l2_vs_fp32": {str(k): v for k, v in sorted(layer_rel_l2.items())},
         "plan": {"jobs": len(cached.jobs), "items": list(cached.abi.n_items), "attached": len(cached.attached)},
         "prefill_s": {m: round(t, 3) for m, t in prefill_s.items()},
         "prefill_speedup": round(prefill_s["request"] / prefill_s["tree"], 2),

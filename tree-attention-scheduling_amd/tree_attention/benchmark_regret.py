@@ -1,7 +1,7 @@
 """Calibration regret: per evaluation shape, the fastest measured plan over every planning method
 and cost-model parameter set, against the plan the fitted model's subset DP (``cube``) makes.
 
-    python -m tree_attention.benchmark_regret [--grid nested|config|reference|headline]
+    python -m tree_attention.benchmark_regret [--grid nested|config|reference|headline|decode]
         [--iters 10] [--output PATH]
 
 Parameter sets: the reference's Ascend 910B defaults (``CostModel()``, schedule.py:29-39) and
@@ -15,6 +15,13 @@ of the K/V pools that span at least 535 MB.
 
 Per shape: ``fitted_cube_us``, ``best_us`` and the (method, parameter set) that gave it, and
 ``regret`` = fitted_cube_us / best_us (1.0 when the fitted DP plan is the fastest measured).
+
+``--grid decode`` times the two decode-step layers of ``shapes.decode_layers`` (the
+decode-plan protocol of scripts/benchmark_decode_plan.py:21-64 and the Qwen3-4B-shaped
+workload's layer), each at one step of its growing tails.  There every (method, parameter
+set) gives two plans, as the protocol's two modes do: ``cached`` (a ``CachedDecodePlan`` over
+the prompt plan, what the decoders run) and ``rebuild`` (the tree with the tails appended,
+planned afresh); the fitted plan is the cached one of the fitted model's ``cube`` schedule.
 """
 from __future__ import annotations
 
@@ -22,6 +29,7 @@ import argparse
 import json
 import math
 import statistics
+import copy
 from dataclasses import asdict
 from pathlib import Path
 
@@ -30,7 +38,7 @@ import torch
 from . import CostModel, schedule, shapes
 from .calibrate import OUT as FITTED_JSON
 from .harness import check, reference_fp32, rotated_pools
-from .kernels import attention_matrix, pack_kv, prepare
+from .kernels import CachedDecodePlan, attention_matrix, pack_kv, prepare
 
 METHODS = ("request", "fixed", "greedy", "cube")
 HQ, HK, D = 32, 8, 128
@@ -74,6 +82,10 @@ def summarize(rows):
             "geomean_regret": math.exp(sum(map(math.log, regrets)) / len(regrets)),
             "median_regret": statistics.median(regrets), "max_regret": max(regrets),
             "fitted_cube_within_2pct": sum(x <= 1.02 for x in regrets),
+            # shapes whose fitted cube plan is more than 3 % slower than the per-request plan
+            "cube_slower_than_request_3pct": [r["shape"] for r in rows
+                                              if r["fitted_cube_us"] > 1.03 * r["request_us"]],
+            "max_cube_over_request": max(r["fitted_cube_us"] / r["request_us"] for r in rows),
             "best_by": _count(r["best_by"] for r in rows),
             "worst": sorted(rows, key=lambda r: -r["regret"])[:5]}
 
@@ -116,10 +128,59 @@ def run_shape(params, spec, sets, iters, seed, dev):
         timed.append((_time(q, pools, prepared, iters), key, who))
     fitted = plan_key(schedule(tree, HQ, HK, D, "cube", sets["fitted"]))
     fitted_us = next(t for t, key, _ in timed if key == fitted)
+    request = plan_key(schedule(tree, HQ, HK, D, "request", sets["fitted"]))
+    request_us = next(t for t, key, _ in timed if key == request)
     best_us, _, best_who = min(timed, key=lambda x: x[0])
     return {"shape": params, "requests": len(tree.paths), "storage_tokens": tree.storage_tokens,
-            "fitted_cube_us": fitted_us, "best_us": best_us, "best_by": best_who[0],
+            "fitted_cube_us": fitted_us, "request_us": request_us, "best_us": best_us, "best_by": best_who[0],
             "best_also": best_who[1:], "regret": fitted_us / best_us, "distinct_plans": len(timed),
+            "plans": [{"us": t, "by": who} for t, _, who in sorted(timed, key=lambda x: x[0])]}
+
+
+def run_decode_layer(name, tree, reserved, generated, sets, iters, seed, dev):
+    """Regret of one decode-step layer: cached and rebuilt plans of every (method, set)."""
+    nreq, prefix = len(tree.paths), tree.storage_tokens
+    g = torch.Generator().manual_seed(seed)
+    t8 = (prefix + nreq * reserved + 7) // 8 * 8
+    q = torch.randn(nreq, HQ, D, generator=g).bfloat16().to(dev)
+    k = torch.randn(t8, HK, D, generator=g).bfloat16().to(dev)
+    v = torch.randn(t8, HK, D, generator=g).bfloat16().to(dev)
+    tails = [[prefix + r * reserved + t for t in range(generated)] for r in range(nreq)]
+    context = type("Context", (), {"paths": [list(p) + t for p, t in zip(tree.paths, tails)]})
+    ref = reference_fp32(q, k, v, context)
+    grown = copy.deepcopy(tree)
+    leaves = [next(i for i, n in enumerate(grown.nodes) if r in n.terminal) for r in range(nreq)]
+    for t in range(generated):
+        grown.extend_leaves(leaves, [prefix + r * reserved + t for r in range(nreq)])
+    kp, vp = pack_kv(k, v)
+    del k, v
+    pools = rotated_pools(kp, vp)
+    plans = {}
+    for method in METHODS:
+        for set_name, model in sets.items():
+            prompt = schedule(tree, HQ, HK, D, method, model)
+            rebuilt = schedule(grown, HQ, HK, D, method, model)
+            for mode, plan in (("cached", prompt), ("rebuild", rebuilt)):
+                key = (mode, plan_key(plan))
+                if key not in plans:
+                    plans[key] = (plan, [])
+                plans[key][1].append((f"{method}/{mode}", set_name))
+    timed = []
+    for key, (plan, who) in plans.items():
+        if key[0] == "cached":
+            prepared = CachedDecodePlan(plan, q, prefix, reserved).update(generated)
+        else:
+            prepared = prepare(plan, q)
+        check(attention_matrix(q, kp, vp, prepared), ref, f"{name} {who[0]}")
+        timed.append((_time(q, pools, prepared, iters), key, who))
+    fitted = ("cached", plan_key(schedule(tree, HQ, HK, D, "cube", sets["fitted"])))
+    fitted_us = next(t for t, key, _ in timed if key == fitted)
+    request_us = next(t for t, key, who in timed if ("request/cached", "fitted") in who)
+    best_us, _, best_who = min(timed, key=lambda x: x[0])
+    return {"shape": {"layer": name, "reserved": reserved, "generated": generated}, "requests": nreq,
+            "storage_tokens": prefix, "fitted_cube_us": fitted_us, "request_us": request_us, "best_us": best_us,
+            "best_by": best_who[0], "best_also": best_who[1:], "regret": fitted_us / best_us,
+            "distinct_plans": len(timed),
             "plans": [{"us": t, "by": who} for t, _, who in sorted(timed, key=lambda x: x[0])]}
 
 
@@ -133,7 +194,7 @@ def grid_of(name):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--grid", default="nested", choices=["nested", "config", "reference", "headline"])
+    ap.add_argument("--grid", default="nested", choices=["nested", "config", "reference", "headline", "decode"])
     ap.add_argument("--iters", type=int, default=10)
     ap.add_argument("--seed", type=int, default=201)
     ap.add_argument("--limit", type=int, default=0, help="run only the first N shapes")
@@ -141,11 +202,17 @@ def main(argv=None):
     args = ap.parse_args(argv)
     dev = torch.device("cuda:0")
     sets = parameter_sets()
-    grid = grid_of(args.grid)[:args.limit or None]
-    run_shape(*grid[0], {"fitted": sets["fitted"]}, 1, args.seed, dev)  # untimed: first loads and calls
+    if args.grid == "decode":
+        layers = list(shapes.decode_layers())[:args.limit or None]
+        run_decode_layer(*layers[0], {"fitted": sets["fitted"]}, 1, args.seed, dev)  # untimed first calls
+        jobs = [lambda layer=layer: run_decode_layer(*layer, sets, args.iters, args.seed, dev) for layer in layers]
+    else:
+        grid = grid_of(args.grid)[:args.limit or None]
+        run_shape(*grid[0], {"fitted": sets["fitted"]}, 1, args.seed, dev)  # untimed: first loads and calls
+        jobs = [lambda p=p, spec=spec: run_shape(p, spec, sets, args.iters, args.seed, dev) for p, spec in grid]
     rows = []
-    for params, spec in grid:
-        row = run_shape(params, spec, sets, args.iters, args.seed, dev)
+    for job in jobs:
+        row = job()
         print(json.dumps({k: v for k, v in row.items() if k != "plans"}), flush=True)
         rows.append(row)
     doc = {"grid": args.grid, "device": torch.cuda.get_device_name(0),

@@ -25,8 +25,12 @@ the same formula is kept and only its parameters are refitted on one MI355X:
   faster (geometric mean), for up to three passes.  The formula is unchanged;
   only its parameters move.
 
-The calibration trees (``shapes.calibration_grid``) share no request count or
-segment length with any evaluation shape.  Every plan is timed over copies of the
+The calibration trees (``shapes.calibration_grid``) and decode-step layers
+(``shapes.decode_calibration_grid``: a prompt tree whose ``CachedDecodePlan``
+carries a growing tail per request, timed at one step, as the decoders run
+it) share no request count or segment length with any evaluation shape.  A
+decode layer's features are its prompt plan's jobs, the part the planner
+decides.  Every plan is timed over copies of the
 K/V pools that span at least 535 MB (``harness.rotated_pools``), as the evaluation
 harnesses time theirs.  The fitted parameters are written
 to ``mi355x_cost_model.json`` next to this module, together with the fit
@@ -47,7 +51,7 @@ import torch
 
 from . import shapes
 from .harness import rotated_pools
-from .kernels import attention_matrix, pack_kv, prepare
+from .kernels import CachedDecodePlan, attention_matrix, pack_kv, prepare
 from .schedule import CostModel, physical_jobs, schedule
 
 METHODS = ("request", "fixed", "greedy", "cube")
@@ -69,13 +73,18 @@ def _estimate(feats, model: CostModel) -> float:
 
 
 class Bench:
-    """Device inputs of one tree and a timer for its plans."""
+    """Device inputs of one tree and a timer for its plans.
 
-    def __init__(self, tree, dev, seed=11):
+    ``decode = (reserved, generated)`` times a plan as a decode step does: a
+    ``CachedDecodePlan`` with ``reserved`` tail tokens per request, updated to
+    ``generated``."""
+
+    def __init__(self, tree, dev, seed=11, decode=None):
         g = torch.Generator().manual_seed(seed)
-        t = tree.storage_tokens
+        t = tree.storage_tokens + (len(tree.paths) * decode[0] if decode else 0)
         t8 = (t + 7) // 8 * 8  # an 8-aligned pool, as the model's pools are
         self.tree = tree
+        self.decode = decode
         self.q = torch.randn(len(tree.paths), HQ, D, generator=g).bfloat16().to(dev)
         k = torch.randn(t8, HK, D, generator=g).bfloat16().to(dev)
         v = torch.randn(t8, HK, D, generator=g).bfloat16().to(dev)
@@ -84,7 +93,11 @@ class Bench:
         self.pools = rotated_pools(kp, vp)
 
     def time_plan(self, plan, iters: int) -> float:
-        prepared = prepare(plan, self.q)
+        if self.decode:
+            reserved, generated = self.decode
+            prepared = CachedDecodePlan(plan, self.q, self.tree.storage_tokens, reserved).update(generated)
+        else:
+            prepared = prepare(plan, self.q)
         for i in range(3):
             attention_matrix(self.q, *self.pools[i % len(self.pools)], prepared)
         torch.cuda.synchronize()
@@ -155,6 +168,8 @@ def tune_terms(model, cube_times, passes=3, factors=(0.25, 0.5, 2.0, 4.0), gain=
 def calibrate(iters=20, kv_splits=(256, 512, 1024), query_rows=(64, 128, 256, 512), log=print):
     dev = torch.device("cuda:0")
     benches = [(name, Bench(shapes.tree(spec), dev)) for name, spec in shapes.calibration_grid()]
+    benches += [(name, Bench(shapes.tree(spec), dev, decode=(reserved, generated)))
+                for name, spec, reserved, generated in shapes.decode_calibration_grid()]
     start = CostModel(bandwidth=5.0e6, cube_flops=1.0e9, task_us=0.5, merge_us=0.01, cube_rows=16,
                       key_tile=64)
     measured = {}
@@ -211,7 +226,8 @@ def main(argv=None):
         "status": "fitted on one MI355X",
         "command": "python -m tree_attention.calibrate " + " ".join(argv or sys.argv[1:]),
         "device": torch.cuda.get_device_name(0),
-        "calibration_grid": [name for name, _ in shapes.calibration_grid()],
+        "calibration_grid": [name for name, _ in shapes.calibration_grid()]
+        + [name for name, *_ in shapes.decode_calibration_grid()],
         "params": best["params"],
         "launch_us": best["launch_us"],
         "fit_rms_log_error": best["fit_rms_log_error"],

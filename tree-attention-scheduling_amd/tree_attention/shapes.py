@@ -19,8 +19,14 @@ Each function returns the ``(parents, lengths, terminals)`` triple accepted by
   requests duplicating the first two leaf paths (35 requests, 20,480 tokens).
 * ``calibration_grid`` -- shapes used only to fit the MI355X cost model; every
   length is disjoint from the evaluation shapes above.
+* ``decode_calibration_grid`` -- decode-step layers (a prompt tree plus a
+  growing tail per request) used only to fit the MI355X cost model, in the
+  form of scripts/calibrate_tiles.py:13-14 (many requests over a short shared
+  root, or private contexts only), at counts and lengths of their own.
 * ``qwen3_4b_workload`` -- the token sequences of the Qwen3-4B-shaped decode
   workload (32 requests over a 2048-token prompt, 4 branches, 8 suffixes each).
+* ``decode_layers`` -- the two decode-step evaluation layers: the protocol of
+  scripts/benchmark_decode_plan.py:21-27 and the Qwen3-4B-shaped workload's.
 """
 from __future__ import annotations
 
@@ -160,6 +166,36 @@ def calibration_grid():
     for requests, context, fraction, depth in product((20, 40, 96), (1500, 6000), (0.5, 0.9), (2, 3)):
         yield (f"deep_r{requests}_{context}_{int(fraction * 100)}_d{depth}",
                grid_tree(requests, context, fraction, depth))
+
+
+def decode_calibration_grid():
+    """Yield ``(name, spec, reserved, generated)``: a prompt tree, the tail tokens reserved per
+    request and the tokens generated so far (a ``CachedDecodePlan`` updated to that step)."""
+    yield "dec_private_r28_736", shared_prefix(28, 0, 736), 15, 9
+    yield "dec_shared_r28_736_44", shared_prefix(28, 736, 44), 15, 9
+    yield "dec_shared_r44_1400_56", shared_prefix(44, 1400, 56), 19, 13
+    yield "dec_shared_r60_480_30", shared_prefix(60, 480, 30), 9, 3
+    yield "dec_shared_r20_2600_36", shared_prefix(20, 2600, 36), 21, 17
+    # a branching prompt: 3 branches of 70 tokens, 12 suffixes of 100 tokens under each
+    parents, lengths, terminals = [-1], [1800], []
+    for _ in range(3):
+        branch = len(parents)
+        parents.append(0)
+        lengths.append(70)
+        for _ in range(12):
+            terminals.append(len(parents))
+            parents.append(branch)
+            lengths.append(100)
+    yield "dec_branch_r36_1800_70_100", (parents, lengths, terminals), 15, 5
+
+
+def decode_layers():
+    """Yield ``(name, tree, reserved, generated)`` of the two decode-step evaluation layers:
+    32 requests over a 1024-token root with 64 private tokens each (the decode-plan protocol,
+    scripts/benchmark_decode_plan.py:21-27) and the Qwen3-4B-shaped workload's prompt tree,
+    each with 16 reserved tail tokens per request, at 8 generated."""
+    yield "protocol_r32_1024_64", tree(shared_prefix(32, 1024, 64)), 16, 8
+    yield "qwen3_4b", KVTree.from_sequences(qwen3_4b_workload()), 16, 8
 
 
 def qwen3_4b_workload(seed: int = 5) -> list:
