@@ -10,8 +10,10 @@ every candidate of the MI355X calibration -- the continuous terms tuned for each
 the chosen one (``fitted``), and each candidate's least-squares terms before the tuning.  Methods: request, fixed, greedy, cube (schedule.py:327-458).
 Identical plans are timed once.  Every plan's output is checked against per-request attention in
 fp32 on the device (atol .008 / rtol .03, scripts/benchmark.py:96) before it is timed; timing is
-the mean of ``--iters`` resident ``attention_matrix`` calls between HIP events, rotating over copies
-of the K/V pools that span at least 535 MB.
+the device time of ``--iters`` resident ``attention_matrix`` calls captured in one HIP graph and
+replayed (``harness.graph_layer_us``), rotating over copies of the K/V pools that span at least
+535 MB.  Eager calls between two events would time the host's submission for the layers of
+10-20 us.
 
 Per shape: ``fitted_cube_us``, ``best_us`` and the (method, parameter set) that gave it, and
 ``regret`` = fitted_cube_us / best_us (1.0 when the fitted DP plan is the fastest measured).
@@ -37,7 +39,7 @@ import torch
 
 from . import CostModel, schedule, shapes
 from .calibrate import OUT as FITTED_JSON
-from .harness import check, reference_fp32, rotated_pools
+from .harness import check, graph_layer_us, reference_fp32, rotated_pools
 from .kernels import CachedDecodePlan, attention_matrix, pack_kv, prepare
 
 METHODS = ("request", "fixed", "greedy", "cube")
@@ -98,16 +100,7 @@ def _count(items):
 
 
 def _time(q, pools, prepared, iters):
-    for i in range(3):
-        attention_matrix(q, *pools[i % len(pools)], prepared)
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(iters):
-        attention_matrix(q, *pools[i % len(pools)], prepared)
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) * 1e3 / iters
+    return graph_layer_us(lambda i: attention_matrix(q, *pools[i % len(pools)], prepared), iters)
 
 
 def run_shape(params, spec, sets, iters, seed, dev):

@@ -12,8 +12,10 @@ the same formula is kept and only its parameters are refitted on one MI355X:
   (``key_tile // 2``).
 * ``kv_split`` and ``max_query_rows`` are structural: for every candidate pair
   the continuous terms are fitted and the pair whose subset-DP (``cube``) plans
-  measure fastest on the calibration grid (geometric mean over its trees) is
-  kept.
+  measure fastest on the calibration grid is kept.  "Fastest" is a weighted
+  geometric mean of the cube plans' times: the static trees share one half of
+  the weight and the decode-step layers the other, so the few decode layers
+  are not outvoted by the many static trees.
 * ``bandwidth``, ``cube_flops``, ``task_us`` and ``merge_us`` are fitted by
   least squares on log((launch + estimated_us) / measured_us) over every plan
   of every method on the calibration grid, with the layer's fixed launch cost
@@ -22,7 +24,7 @@ the same formula is kept and only its parameters are refitted on one MI355X:
 * The least-squares terms predict times, not which plan is fastest.  A coordinate
   search then scales one term at a time by 1/4, 1/2, 2 or 4 and keeps a change
   when the measured ``cube`` plans of the calibration grid get at least 1 %
-  faster (geometric mean), for up to three passes.  The formula is unchanged;
+  faster (the same weighted geometric mean), for up to three passes.  The formula is unchanged;
   only its parameters move.
 
 The calibration trees (``shapes.calibration_grid``) and decode-step layers
@@ -32,7 +34,8 @@ it) share no request count or segment length with any evaluation shape.  A
 decode layer's features are its prompt plan's jobs, the part the planner
 decides.  Every plan is timed over copies of the
 K/V pools that span at least 535 MB (``harness.rotated_pools``), as the evaluation
-harnesses time theirs.  The fitted parameters are written
+harnesses time theirs, on the device alone: ``iters`` layers captured in one
+HIP graph and replayed (``harness.graph_layer_us``).  The fitted parameters are written
 to ``mi355x_cost_model.json`` next to this module, together with the fit
 residuals and the command that produced them.
 """
@@ -50,7 +53,7 @@ import numpy as np
 import torch
 
 from . import shapes
-from .harness import rotated_pools
+from .harness import graph_layer_us, rotated_pools
 from .kernels import CachedDecodePlan, attention_matrix, pack_kv, prepare
 from .schedule import CostModel, physical_jobs, schedule
 
@@ -98,16 +101,8 @@ class Bench:
             prepared = CachedDecodePlan(plan, self.q, self.tree.storage_tokens, reserved).update(generated)
         else:
             prepared = prepare(plan, self.q)
-        for i in range(3):
-            attention_matrix(self.q, *self.pools[i % len(self.pools)], prepared)
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for i in range(iters):
-            attention_matrix(self.q, *self.pools[i % len(self.pools)], prepared)
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) * 1e3 / iters
+        return graph_layer_us(lambda i: attention_matrix(self.q, *self.pools[i % len(self.pools)], prepared),
+                              iters)
 
 
 def fit_terms(samples, model: CostModel):
@@ -140,22 +135,26 @@ def _geomean(values):
     return float(np.exp(np.mean(np.log(values))))
 
 
-def tune_terms(model, cube_times, passes=3, factors=(0.25, 0.5, 2.0, 4.0), gain=0.01):
+def _weighted_geomean(values, weights):
+    return float(np.exp(np.dot(weights, np.log(values)) / np.sum(weights)))
+
+
+def tune_terms(model, cube_times, passes=3, factors=(0.25, 0.5, 2.0, 4.0), gain=0.01, score=_geomean):
     """Coordinate search of the continuous terms on measured plan quality.
 
     ``cube_times(model)`` returns the measured times of ``model``'s cube plans on the
     calibration trees.  Each pass tries every term scaled by every factor and keeps
-    the best change if it lowers their geometric mean by at least ``gain``.
-    Returns (model, geometric mean, steps taken).
+    the best change if it lowers their ``score`` (geometric mean by default) by at
+    least ``gain``.  Returns (model, score, steps taken).
     """
-    best, best_s = model, _geomean(cube_times(model))
+    best, best_s = model, score(cube_times(model))
     steps = []
     for _ in range(passes):
         trial = None
         for f in FIT_FIELDS:
             for k in factors:
                 m = replace(best, **{f: getattr(best, f) * k})
-                s_ = _geomean(cube_times(m))
+                s_ = score(cube_times(m))
                 if s_ < best_s * (1 - gain) and (trial is None or s_ < trial[1]):
                     trial = (m, s_, (f, k))
         if trial is None:
@@ -170,6 +169,13 @@ def calibrate(iters=20, kv_splits=(256, 512, 1024), query_rows=(64, 128, 256, 51
     benches = [(name, Bench(shapes.tree(spec), dev)) for name, spec in shapes.calibration_grid()]
     benches += [(name, Bench(shapes.tree(spec), dev, decode=(reserved, generated)))
                 for name, spec, reserved, generated in shapes.decode_calibration_grid()]
+    # the static trees and the decode-step layers weigh half each in the score
+    n_dec = sum(b.decode is not None for _, b in benches)
+    weights = np.array([0.5 / n_dec if b.decode else 0.5 / (len(benches) - n_dec) for _, b in benches])
+
+    def score(times):
+        return _weighted_geomean(times, weights)
+
     start = CostModel(bandwidth=5.0e6, cube_flops=1.0e9, task_us=0.5, merge_us=0.01, cube_rows=16,
                       key_tile=64)
     measured = {}
@@ -195,8 +201,8 @@ def calibrate(iters=20, kv_splits=(256, 512, 1024), query_rows=(64, 128, 256, 51
 
             def cube_times(m):
                 return [measure(name, b, schedule(b.tree, HQ, HK, D, "cube", m)) for name, b in benches]
-            lsq_geomean = _geomean(cube_times(model))
-            model, _, steps = tune_terms(model, cube_times)
+            lsq_score = score(cube_times(model))
+            model, _, steps = tune_terms(model, cube_times, score=score)
             cube = {name: measure(name, b, schedule(b.tree, HQ, HK, D, "cube", model)) for name, b in benches}
             req = {name: measure(name, b, schedule(b.tree, HQ, HK, D, "request", model)) for name, b in benches}
             cube_us, req_us = sum(cube.values()), sum(req.values())
@@ -204,14 +210,15 @@ def calibrate(iters=20, kv_splits=(256, 512, 1024), query_rows=(64, 128, 256, 51
             err_lsq = [math.log((launch + _estimate(f, fitted)) / t) for f, t in samples]
             row = {"params": asdict(model), "least_squares_params": asdict(fitted), "tuning_steps": steps,
                    "launch_us": launch, "cube_total_us": cube_us, "request_total_us": req_us,
-                   "cube_geomean_us": _geomean(list(cube.values())), "least_squares_cube_geomean_us": lsq_geomean,
+                   "cube_geomean_us": _geomean(list(cube.values())), "cube_score_us": score(list(cube.values())),
+                   "least_squares_cube_score_us": lsq_score,
                    "cube_us": cube, "fit_rms_log_error": float(np.sqrt(np.mean(np.square(err)))),
                    "least_squares_rms_log_error": float(np.sqrt(np.mean(np.square(err_lsq)))),
                    "samples": len(samples), "plans_timed": len(measured)}
             candidates.append(row)
             log(json.dumps(row))
-    # every calibration tree counts alike: geometric mean of the cube plans' times
-    best = min(candidates, key=lambda r: r["cube_geomean_us"])
+    # the static trees and the decode layers count alike: weighted geometric mean of the cube plans' times
+    best = min(candidates, key=lambda r: r["cube_score_us"])
     return best, candidates
 
 
@@ -233,6 +240,7 @@ def main(argv=None):
         "fit_rms_log_error": best["fit_rms_log_error"],
         "cube_total_us": best["cube_total_us"],
         "cube_geomean_us": best["cube_geomean_us"],
+        "cube_score_us": best["cube_score_us"],
         "request_total_us": best["request_total_us"],
         "candidates": candidates,
         "seconds": round(time.time() - t0, 1),

@@ -11,6 +11,12 @@ dtype).  The harnesses check every timed configuration against it with the
 reference's device tolerance (atol .008 / rtol .03, scripts/benchmark.py:96)
 and report the relative L2 error; the CPU oracle comparison of the same shapes
 is the GPU test suite's.  Operands are fp32 and contiguous.
+
+``graph_layer_us`` times layers on the device alone: a decode-sized layer
+(10-20 us) is shorter than the host's submission of one ``attention_matrix``
+call, so a loop of eager calls between two events measures the host.  It
+captures ``count`` calls (rotating over the pools) in one HIP graph and times
+replays of it, as a decode step that runs ahead of the device sees them.
 """
 from __future__ import annotations
 
@@ -55,3 +61,33 @@ def check(out: torch.Tensor, ref32: torch.Tensor, what: str) -> dict:
     diff = out.float() - ref32
     return {"max_abs_error": diff.abs().max().item(),
             "rel_l2": (diff.norm() / ref32.norm().clamp_min(1e-30)).item()}
+
+
+def graph_layer_us(layer, count: int, replays: int = 5) -> float:
+    """Mean device time of ``layer(i)``, i = 0..count-1, from replays of one HIP graph of them.
+
+    ``layer`` must neither allocate device memory nor synchronise (``attention_matrix``
+    writes the plan's own output buffer).  The graph is captured on a side stream.
+    """
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for i in range(min(count, 3)):  # first calls: library and code-object loads
+            layer(i)
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for i in range(count):
+            layer(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    del graph
+    return start.elapsed_time(end) * 1e3 / (replays * count)
