@@ -498,6 +498,18 @@ struct PipeMath {
         }
     }
 
+    // The running maxima from the job's first scored step: O and z are still
+    // zero, so the maxima are set without the pass over O that rescale makes
+    // (the values equal rescale's from the initial state).
+    __device__ void first_max(float c, float rc) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const float mn = xor_max(lm[nb]) * c;
+            m[nb] = mn;
+            thr[nb] = (mn + TAU) * rc;
+        }
+    }
+
     // Raise the running maxima where a score of the staged step exceeds them
     // by more than TAU (wave-uniform branch, rare after the first step).
     __device__ void rescale(float c, float rc) {  // rc = 1 / c
@@ -590,7 +602,10 @@ struct PipeMath {
             f32x4 sn[NB][2];
             TM::load_k(st, of, base, kf);
             TM::qk(kf, qf, sn);
-            finish_scores<true>(sn, lo - base, hi - base, g4);
+            if (lo <= base && hi >= base + 32)  // wave-uniform: every token of the step is the segment's
+                finish_scores<false>(sn, 0, 32, g4);
+            else
+                finish_scores<true>(sn, lo - base, hi - base, g4);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
                 if (!((keep >> nb) & 1)) lm[nb] = NEG_INF;
@@ -741,7 +756,7 @@ __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__r
         TM::load_k(lds, of, 0, acc.kf);
         TM::qk(acc.kf, qf, s0);
         acc.template finish_scores<true>(s0, kst - tb0, kend - tb0, g4);
-        acc.rescale(c, rc);
+        acc.first_max(c, rc);
         if (nsteps > 1) TM::load_k(lds, of, 32, acc.kf);
     }
 
@@ -795,8 +810,10 @@ __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__r
             __builtin_amdgcn_s_barrier();  // the round's tiles landed
 #pragma unroll
             for (int k = 0; k < XM; ++k) {
-                const int rlo = rec[3 + XF * k] - wrow0;  // segment rows in this wave: [rlo, rlo + rows)
-                if (xn[k] > 0 && active && rlo >= 0 && rlo < 16 * NB) {
+                // segment rows relative to this wave's: [rlo, rlo + rows); with 16 rows per
+                // wave (NB = 1) a segment may span two waves, each attends its own rows
+                const int rlo = rec[3 + XF * k] - wrow0;
+                if (xn[k] > 0 && active && rlo < 16 * NB && rlo + rec[4 + XF * k] > 0) {
                     for (int i = max(0, r0 - xfirst[k]); i < xn[k] && xfirst[k] + i < r1; ++i) {
                         const int t0 = (xs[k] & ~7) + i * T::TT;
                         acc.tail_tile(tile_stage(xfirst[k] + i), qf, of, max(0, xs[k] - t0), min(T::TT, xe[k] - t0),
@@ -819,10 +836,23 @@ __device__ __forceinline__ void pipe_item(const SegParams &p, const int32_t *__r
     }
 }
 
+// A 256-row work item whose job has at most 8 NW rows from the item's first
+// row on runs 16 rows per wave, so that every wave computes (two per SIMD)
+// instead of half of them 32 rows each; the arithmetic of every row is the same.
+template <int D, bool FP16, int NW>
+__device__ __forceinline__ void pipe_item_rows(const SegParams &p, const int32_t *__restrict__ items, int item,
+                                               u16 *lds, int tid) {
+    const int job = items[3 * item], row0 = items[3 * item + 1];
+    if (p.qlen[job] * p.group - row0 <= 16 * NW)
+        pipe_item<D, FP16, NW, 1>(p, items, item, lds, tid);
+    else
+        pipe_item<D, FP16, NW, 2>(p, items, item, lds, tid);
+}
+
 template <int D, bool FP16, int NW>
 __global__ __launch_bounds__(64 * NW) void seg_pipe_kernel(SegParams p) {
     __shared__ __attribute__((aligned(16))) u16 lds[TA_PIPE_STAGES * Tile<D>::ELEMS];
-    pipe_item<D, FP16, NW>(p, p.items, xcd_item(blockIdx.x, gridDim.x), lds, threadIdx.x);
+    pipe_item_rows<D, FP16, NW>(p, p.items, xcd_item(blockIdx.x, gridDim.x), lds, threadIdx.x);
 }
 
 // Work items of several kinds of one layer in one launch of 512-thread
@@ -841,7 +871,7 @@ __global__ __launch_bounds__(512) void seg_mix_kernel(MixParams mp) {
     const int b = blockIdx.x, tid = threadIdx.x;
     if (b < mp.base[1]) {
         if (b >= mp.n[0]) return;
-        pipe_item<D, FP16, 8>(mp.p, mp.items[0], xcd_item(b, mp.n[0]), lds, tid);
+        pipe_item_rows<D, FP16, 8>(mp.p, mp.items[0], xcd_item(b, mp.n[0]), lds, tid);
     } else if (b < mp.base[2]) {
         const int lb = b - mp.base[1];
         if (lb >= mp.n[1]) return;
