@@ -247,9 +247,10 @@ def test_subclassed_cost_model_is_honoured():
 
 
 def test_calibration_coordinate_search():
-    """calibrate.tune_terms scales one continuous term at a time (1/4 .. 4x) and keeps the best
-    change while the measured cube plans get at least 1 % faster: on a synthetic measurement
-    whose optimum is task_us = 0.02 and bandwidth = 8e6 it walks there and stops."""
+    """calibrate.tune_terms scales one continuous term at a time (1/4 .. 4x), or sets a per-job
+    term to an absolute level, and keeps the best change while the measured cube plans get at
+    least 1 % faster: on a synthetic measurement whose optimum is task_us = 0.02 and bandwidth
+    = 8e6 it walks there by factors and stops; from merge_us at 1e-4 it reaches 0.1 in one step."""
     import math
     from tree_attention.calibrate import tune_terms
 
@@ -257,10 +258,14 @@ def test_calibration_coordinate_search():
         return [1.0 + math.log(m.task_us / 0.02) ** 2 + 0.5 * math.log(m.bandwidth / 8e6) ** 2] * 3
 
     start = CostModel(bandwidth=2e6, cube_flops=1e9, task_us=0.32, merge_us=0.01)
-    best, score, steps = tune_terms(start, times, passes=5)
+    best, score, steps = tune_terms(start, times, passes=5, levels={})
     assert math.isclose(best.task_us, 0.02) and math.isclose(best.bandwidth, 8e6)
     assert best.cube_flops == 1e9 and best.merge_us == 0.01 and math.isclose(score, 1.0)
     assert steps == [("task_us", 0.25), ("task_us", 0.25), ("bandwidth", 4.0)]
     # a change under 1 % is not taken
     flat, _, none = tune_terms(start, lambda m: [1.0 + 1e-3 * m.task_us])
     assert flat == start and none == []
+    # absolute levels reach a per-job term far from its start (a fit left at its bound)
+    pinned = CostModel(bandwidth=8e6, cube_flops=1e9, task_us=0.02, merge_us=1e-4)
+    best, score, steps = tune_terms(pinned, lambda m: [1.0 + math.log(m.merge_us / 0.1) ** 2] * 3)
+    assert best.merge_us == 0.1 and steps == [("merge_us", "=", 0.1)] and math.isclose(score, 1.0)

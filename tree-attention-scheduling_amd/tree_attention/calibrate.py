@@ -22,9 +22,12 @@ the same formula is kept and only its parameters are refitted on one MI355X:
   as a nuisance term that the planner does not use.  Plans of ``greedy`` / ``cube`` depend on the
   parameters, so the fit is repeated with plans re-made from the fitted values.
 * The least-squares terms predict times, not which plan is fastest.  A coordinate
-  search then scales one term at a time by 1/4, 1/2, 2 or 4 and keeps a change
-  when the measured ``cube`` plans of the calibration grid get at least 1 %
-  faster (the same weighted geometric mean), for up to three passes.  The formula is unchanged;
+  search then scales one term at a time by 1/4, 1/2, 2 or 4, or sets a per-job
+  term (``task_us``, ``merge_us``) to one of a few absolute levels (3 ns .. 1 us),
+  and keeps a change when the measured ``cube`` plans of the calibration grid get
+  at least 1 % faster (the same weighted geometric mean), for up to three passes.
+  The levels matter because the fit's layer-constant term absorbs the per-job
+  costs, which it then leaves at their lower bounds.  The formula is unchanged;
   only its parameters move.
 
 The calibration trees (``shapes.calibration_grid``) and decode-step layers
@@ -139,24 +142,36 @@ def _weighted_geomean(values, weights):
     return float(np.exp(np.dot(weights, np.log(values)) / np.sum(weights)))
 
 
-def tune_terms(model, cube_times, passes=3, factors=(0.25, 0.5, 2.0, 4.0), gain=0.01, score=_geomean):
+# absolute values the coordinate search also tries for the per-job terms (us): the
+# least-squares fit leaves them at their bounds when the layer's fixed cost absorbs them
+LEVELS = {"task_us": (0.003, 0.01, 0.03, 0.1, 0.3, 1.0), "merge_us": (0.003, 0.01, 0.03, 0.1, 0.3, 1.0)}
+
+
+def tune_terms(model, cube_times, passes=3, factors=(0.25, 0.5, 2.0, 4.0), gain=0.01, score=_geomean,
+               levels=None):
     """Coordinate search of the continuous terms on measured plan quality.
 
     ``cube_times(model)`` returns the measured times of ``model``'s cube plans on the
-    calibration trees.  Each pass tries every term scaled by every factor and keeps
-    the best change if it lowers their ``score`` (geometric mean by default) by at
-    least ``gain``.  Returns (model, score, steps taken).
+    calibration trees.  Each pass tries every term scaled by every factor, and set to
+    each of its ``levels`` (absolute values, ``LEVELS`` by default), and keeps the best
+    change if it lowers their ``score`` (geometric mean by default) by at least
+    ``gain``.  Returns (model, score, steps taken); a step is (term, factor) or
+    (term, "=", value).
     """
+    levels = LEVELS if levels is None else levels
     best, best_s = model, score(cube_times(model))
     steps = []
     for _ in range(passes):
         trial = None
         for f in FIT_FIELDS:
-            for k in factors:
-                m = replace(best, **{f: getattr(best, f) * k})
+            moves = [((f, k), replace(best, **{f: getattr(best, f) * k})) for k in factors]
+            moves += [((f, "=", x), replace(best, **{f: x})) for x in levels.get(f, ())]
+            for step, m in moves:
+                if m == best:
+                    continue
                 s_ = score(cube_times(m))
                 if s_ < best_s * (1 - gain) and (trial is None or s_ < trial[1]):
-                    trial = (m, s_, (f, k))
+                    trial = (m, s_, step)
         if trial is None:
             break
         best, best_s = trial[0], trial[1]

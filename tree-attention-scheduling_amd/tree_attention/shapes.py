@@ -139,6 +139,10 @@ def calibration_grid():
     for requests in (6, 20, 40):
         for private in (700, 2000):
             yield f"private_r{requests}_{private}", shared_prefix(requests, 0, private)
+    # short shared prefixes under long private contexts, where sharing saves little and
+    # every shared job adds a partial slot per request to merge
+    for requests, root, private in ((28, 300, 940), (44, 700, 2300), (60, 1100, 3900), (20, 180, 1300)):
+        yield f"shared_r{requests}_{root}_{private}", shared_prefix(requests, root, private)
     # large shapes, where launch overheads are a small part of the layer
     for requests, root, private in ((112, 7000, 50), (80, 6000, 150), (72, 3500, 90)):
         yield f"shared_r{requests}_{root}_{private}", shared_prefix(requests, root, private)
