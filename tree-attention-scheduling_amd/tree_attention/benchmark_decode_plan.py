@@ -2,7 +2,7 @@
 and the ``decode`` aggregation of scripts/analyze_planning.py:19-39).
 
     python -m tree_attention.benchmark_decode_plan [--steps 16] [--seeds 301 302 303]
-        [--planner auto|cpp|python] [--output PATH]
+        [--planner auto|cpp|python] [--cost-model reference|mi355x] [--output PATH]
 
 Workload (scripts/benchmark_decode_plan.py:21-27): 32 requests sharing a
 1024-token root, each with a private 64-token node; bf16 Q [32, 32, 128] and
@@ -24,7 +24,10 @@ tree (the ``request`` method, a different kernel path) within the
 reference's device tolerance (atol .008, rtol .03); the oracle comparison of
 the same protocol is in the GPU test suite.
 
-``--planner`` selects the greedy / cube decision code of ``schedule``
+``--cost-model`` selects the planner's parameters: ``reference`` (the
+reference's defaults, as its script plans) or ``mi355x`` (the fitted MI355X
+parameters the decoders of this package use).  ``--planner`` selects the
+greedy / cube decision code of ``schedule``
 (``cpp``: libtree_plan.so, ``python``: the Python planner; both give the same
 plans).  Output: one JSON object per (method, mode, seed) as it finishes,
 then the aggregate over seeds in the reference's ``results/decode_plan.json``
@@ -42,7 +45,7 @@ from statistics import median
 
 import torch
 
-from . import KVTree, schedule
+from . import CostModel, KVTree, schedule
 from .kernels import CachedDecodePlan, attention_matrix, pack_kv, prepare
 
 REQUESTS, ROOT, PRIVATE, HQ, HK, D = 32, 1024, 64, 32, 8, 128
@@ -59,7 +62,7 @@ def _sync_time(fn):
     return out, (time.perf_counter() - t0) * 1e6
 
 
-def run_seed(seed, steps, native, dev, log):
+def run_seed(seed, steps, native, dev, log, model=None):
     base = KVTree.synthetic([-1] + [0] * REQUESTS, [ROOT] + [PRIVATE] * REQUESTS, list(range(1, REQUESTS + 1)))
     prefix = base.storage_tokens
     g = torch.Generator().manual_seed(seed)
@@ -67,7 +70,7 @@ def run_seed(seed, steps, native, dev, log):
     k = torch.randn(prefix + REQUESTS * steps, HK, D, generator=g).bfloat16().to(dev)
     v = torch.randn(k.shape, generator=g).bfloat16().to(dev)
     kp, vp = pack_kv(k, v)
-    warm = CachedDecodePlan(schedule(base, method="fixed", native=native), q, prefix, steps)
+    warm = CachedDecodePlan(schedule(base, method="fixed", model=model, native=native), q, prefix, steps)
     attention_matrix(q, kp, vp, warm.update(1))
     torch.cuda.synchronize()
     del warm
@@ -78,7 +81,8 @@ def run_seed(seed, steps, native, dev, log):
             leaves = list(range(1, REQUESTS + 1))
             if mode == "cached":
                 cached, initial_us = _sync_time(
-                    lambda: CachedDecodePlan(schedule(tree, method=method, native=native), q, prefix, steps))
+                    lambda: CachedDecodePlan(schedule(tree, method=method, model=model, native=native), q, prefix,
+                                             steps))
             else:
                 cached, initial_us = None, _sync_time(lambda: None)[1]
             costs = []
@@ -86,7 +90,7 @@ def run_seed(seed, steps, native, dev, log):
                 if mode == "rebuild":
                     def plan_step():
                         tree.extend_leaves(leaves, [prefix + r * steps + step for r in range(REQUESTS)])
-                        return prepare(schedule(tree, method=method, native=native), q)
+                        return prepare(schedule(tree, method=method, model=model, native=native), q)
                     prepared, planning_us = _sync_time(plan_step)
                 else:
                     prepared, planning_us = _sync_time(lambda: cached.update(step + 1))
@@ -137,14 +141,17 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=16)
     ap.add_argument("--seeds", type=int, nargs="+", default=[301, 302, 303])
     ap.add_argument("--planner", choices=sorted(NATIVE), default="auto")
+    ap.add_argument("--cost-model", choices=["reference", "mi355x"], default="reference")
     ap.add_argument("--output", default=None)
     args = ap.parse_args(argv)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    model = CostModel.mi355x() if args.cost_model == "mi355x" else CostModel()
     runs = []
     for seed in args.seeds:
-        runs += run_seed(seed, args.steps, NATIVE[args.planner], dev, lambda s: print(s, flush=True))
-    result = {"inputs": [f"seed {s}" for s in args.seeds], "planner": args.planner, "results": aggregate(runs)}
+        runs += run_seed(seed, args.steps, NATIVE[args.planner], dev, lambda s: print(s, flush=True), model)
+    result = {"inputs": [f"seed {s}" for s in args.seeds], "planner": args.planner, "cost_model": args.cost_model,
+              "results": aggregate(runs)}
     if args.output:
         Path(args.output).write_text(json.dumps(result, indent=2))
     print(json.dumps(result), flush=True)
