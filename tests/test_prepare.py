@@ -455,3 +455,24 @@ def test_one_tile_chunks_lengthen_when_the_lowering_keeps_its_kinds():
     assert b.jobs == CachedDecodePlan(schedule(qt, 32, 8, 128, "cube", CostModel.mi355x()), qq, t0, 16).prepared.jobs
     assert [(j.requests, j.tokens) for j in a.jobs] == [(j.requests, j.tokens) for j in b.jobs]
     assert list(a.abi.n_items) == list(b.abi.n_items)
+
+
+def test_wide_jobs_fill_the_gpu_as_64_row_groups():
+    """A 128-row root whose 256-row items, cut into one-tile chunks, fill more than a quarter but
+    at most half of the 256 CUs runs as two 64-row request groups per chunk instead (the
+    decode-plan protocol's layer: 32 requests x 1024 shared tokens, 16 chunks x 8 KV heads = 128
+    256-row items -> 64-row groups); a root long enough to fill the GPU in 256-row items keeps
+    them (the Qwen3-4B-shaped layer's 2048-token root: 256 items, tails attached)."""
+    from tree_attention import CostModel, schedule, shapes
+    from tree_attention.kernels import CachedDecodePlan
+    layers = {name: (tree, reserved) for name, tree, reserved, _ in shapes.decode_layers()}
+    tree, reserved = layers["protocol_r32_1024_64"]
+    q = torch.zeros(len(tree.paths), 32, 128, dtype=torch.bfloat16)
+    p = CachedDecodePlan(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q, tree.storage_tokens, reserved)
+    n = list(p.prepared.abi.n_items)
+    assert n[_native.TA_LARGE256] == 0 and n[_native.TA_LARGE64] == 128
+    assert all(len(j.requests) <= 16 for j in p.prepared.jobs)
+    tree, reserved = layers["qwen3_4b"]
+    p = CachedDecodePlan(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q, tree.storage_tokens, reserved)
+    n = list(p.prepared.abi.n_items)
+    assert n[_native.TA_LARGE256] == 256 and n[_native.TA_LARGE64] == 0 and p.prepared.attached

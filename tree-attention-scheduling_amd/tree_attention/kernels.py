@@ -621,16 +621,27 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
                 large = [j for j in large if id(j) not in gone]
         return small, large, attached
 
-    def lowering(min_tiles):
-        """``lower``, then one large-job kind and routing: (small, large, attachments)."""
+    def lowering(min_tiles, fill=None):
+        """``lower``, then one large-job kind and routing: (small, large, attachments, fill).
+
+        ``fill``: whether the wider jobs run as 64-row groups to fill the GPU (decided from
+        one-tile chunks when None)."""
         small, large, attached = lower(small0, large0, min_tiles)
         # One large-job kind: when 64-row items run anyway and every wider job holds at most
         # consolidate_rows rows, the wider jobs run as 64-row request groups in the same kind
         # (one launch and its start-up less; their K/V is read once per group).
         per64 = 64 // group
         wide = [j for j in large0 if len(j.requests) * group > 64]
+        # ... and also when the wider jobs' 256-row items, cut into one-tile chunks, fill more
+        # than a quarter but at most half of the CUs: two 64-row groups per job read its K/V
+        # twice but fill up to all of them
+        if fill is None:
+            items256 = sum(-(-len(j.requests) * group // 256) for j in large
+                           if _large_kind(len(j.requests) * group, tile_rows) == _native.TA_LARGE256) * kvheads
+            fill = min_tiles == 1 and n_cu // 4 < items256 <= n_cu // 2
         if (consolidate_rows and per64 and wide and all(len(j.requests) * group <= consolidate_rows for j in wide)
-                and any(_large_kind(len(j.requests) * group, tile_rows) == _native.TA_LARGE64 for j in large)):
+                and (any(_large_kind(len(j.requests) * group, tile_rows) == _native.TA_LARGE64 for j in large)
+                     or fill)):
             split = []
             for j in large0:
                 if len(j.requests) * group > 64:
@@ -642,20 +653,20 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
                                            [j for j in split if len(j.requests) * group > SMALL_ROWS], min_tiles)
         if small and routed and sum(map(_tiles, routed)) * kvheads <= route_items:
             small, large, attached = small0 + routed, [], {}
-        return small, large, attached
+        return small, large, attached, fill
 
     def kinds(small, large):
         return ({-1} if small else set()) | {_large_kind(len(j.requests) * group, tile_rows) for j in large}
 
     large0 = large
-    small, large, attached = lowering(1)
+    small, large, attached, fill = lowering(1)
     if large_min_tiles > 1 and any(len(j.tokens) < large_min_tiles * TOKEN_QUANTUM for j in large):
         # A one-tile chunk costs a work item's start-up and a partial slot: chunks of
         # large_min_tiles tiles are taken when the lowering keeps its kernel kinds and
         # leaves no more small jobs (an item's latency, not its tiles, sets its time).
-        alt = lowering(large_min_tiles)
+        alt = lowering(large_min_tiles, fill)
         if kinds(*alt[:2]) == kinds(small, large) and len(alt[0]) <= len(small):
-            small, large, attached = alt
+            small, large, attached = alt[:3]
     # Tails (a request's only small job) stay whole when they alone fill the GPU,
     # so that their work items can merge their requests.
     owners = {}
