@@ -476,3 +476,16 @@ def test_wide_jobs_fill_the_gpu_as_64_row_groups():
     p = CachedDecodePlan(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q, tree.storage_tokens, reserved)
     n = list(p.prepared.abi.n_items)
     assert n[_native.TA_LARGE256] == 256 and n[_native.TA_LARGE64] == 0 and p.prepared.attached
+
+
+def test_large_recut_keeps_one_round_of_items():
+    """A large-kind re-cut that would give a few more items than CUs (a second round of work
+    items for the surplus) takes the next longer chunks when one round of them is shorter than
+    two rounds of the shorter chunks: 32 requests over a 4096-token context, 99 % shared in three
+    levels, lowers to 192 64-row items instead of 272."""
+    from tree_attention import CostModel, schedule, shapes
+    tree = shapes.tree(shapes.grid_tree(32, 4096, 0.99, 3))
+    q = torch.zeros(len(tree.paths), 32, 128, dtype=torch.bfloat16)
+    p = prepare(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q)
+    assert p.abi.n_items[_native.TA_LARGE64] == 192
+    assert _covers_paths_plan(p, schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), len(tree.paths))

@@ -346,7 +346,7 @@ def _fuse_same_tokens(jobs, group, min_rows):
     return out
 
 
-def _recut(jobs, items_per_chunk, target_items, is_fixed, min_tiles=1, floor_items=0):
+def _recut(jobs, items_per_chunk, target_items, is_fixed, min_tiles=1, floor_items=0, one_round=False):
     """Execution jobs for one kernel kind: runs of consecutive jobs over the same
     requests and contiguous tokens are cut again into near-equal chunks, as long
     as possible while the kind still gets ``target_items`` work items (one
@@ -355,6 +355,10 @@ def _recut(jobs, items_per_chunk, target_items, is_fixed, min_tiles=1, floor_ite
     Jobs for which ``is_fixed(job)`` holds (growing decode tails, tails that
     merge their request) are left alone.  Chunks are at least ``min_tiles``
     tiles long whenever that still gives ``floor_items`` work items.
+    ``one_round``: ``target_items`` items run at once (one per CU), so a cut that
+    gives a few more than that runs a second round of items for them; the next
+    longer cut, one round of longer chunks, is taken when its chunks are shorter
+    than the rounds' chunks end to end.
     """
     runs = []  # [requests, first token, length, fixed]
     for job in jobs:
@@ -388,6 +392,10 @@ def _recut(jobs, items_per_chunk, target_items, is_fixed, min_tiles=1, floor_ite
             lo = mid
         else:
             hi = mid
+    if one_round and hi > lo:
+        rounds = -(-count(lo * TOKEN_QUANTUM) // target_items)
+        if rounds > 1 and hi < rounds * lo:  # count(hi) < target_items: one round
+            lo = hi
     if lo < min_tiles and count(min_tiles * TOKEN_QUANTUM) >= floor_items:
         lo = min_tiles
     limit = lo * TOKEN_QUANTUM
@@ -602,7 +610,7 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     def lower(small, large, min_tiles):
         """Re-cut, order and attach: (small jobs, large jobs, attachments)."""
         large = _recut(large, lambda r: -(-len(r) * group // _native.KIND_ROWS[_large_kind(len(r) * group, tile_rows)])
-                       * kvheads, large_target, growing, min_tiles, large_target // 2)
+                       * kvheads, large_target, growing, min_tiles, large_target // 2, one_round=True)
         # chunks of one token range side by side: a root split into request groups then gives
         # request r its k-th slot at r + k * (requests of a chunk), the layout the merge computes
         large.sort(key=lambda j: (j.tokens[0], j.requests[0]))
