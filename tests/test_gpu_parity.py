@@ -450,11 +450,13 @@ def test_cached_decode_plan_steps(device):
 
 @pytest.mark.parametrize("model_name", ["mi355x", "mi355x-like"])
 def test_attached_growing_tails(model_name, device):
-    """The decode-plan protocol (32 requests, 1024 + 64 prompt, 16 reserved tail tokens each)
-    with the private and growing tails attached to the root's work items: the layer is one
-    segment launch plus the merge, and each step's tail length is read from the attachment
-    records that update() rewrites.  Steps 0, 1, 8 and 16 against the oracle."""
-    base = shapes.tree(shapes.shared_prefix(32, 1024, 64))
+    """The decode-plan protocol's form with a 2048-token root (32 requests, 2048 + 64 prompt,
+    16 reserved tail tokens each), whose 256-row root items fill the GPU, so that the private
+    and growing tails attach to them: the layer is one segment launch plus the merge, and each
+    step's tail length is read from the attachment records that update() rewrites.  (The
+    protocol's own 1024-token root runs as 64-row groups, see test_prepare.)  Steps 0, 1, 8
+    and 16 against the oracle."""
+    base = shapes.tree(shapes.shared_prefix(32, 2048, 64))
     prefix = base.storage_tokens
     steps = 16
     g = torch.Generator().manual_seed(307)
