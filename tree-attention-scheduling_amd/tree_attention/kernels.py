@@ -641,12 +641,16 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
         per64 = 64 // group
         wide = [j for j in large0 if len(j.requests) * group > 64]
         # ... and also when the wider jobs' 256-row items, cut into one-tile chunks, fill more
-        # than a quarter but at most half of the CUs: two 64-row groups per job read its K/V
-        # twice but fill up to all of them
+        # than a quarter but at most half of the CUs and every small job is one tile long (the
+        # private suffixes and growing tails of a decode step): two 64-row groups per job read
+        # its K/V twice but fill up to all of them, and the one-tile small jobs run beside them
+        # instead of in sequence on the 256-row items.  Longer small jobs stay with the
+        # 256-row items, whose attachments and single merge they need.
         if fill is None:
             items256 = sum(-(-len(j.requests) * group // 256) for j in large
                            if _large_kind(len(j.requests) * group, tile_rows) == _native.TA_LARGE256) * kvheads
-            fill = min_tiles == 1 and n_cu // 4 < items256 <= n_cu // 2
+            fill = (min_tiles == 1 and n_cu // 4 < items256 <= n_cu // 2
+                    and all(_tiles(j) <= 1 for j in small0))
         if (consolidate_rows and per64 and wide and all(len(j.requests) * group <= consolidate_rows for j in wide)
                 and (any(_large_kind(len(j.requests) * group, tile_rows) == _native.TA_LARGE64 for j in large)
                      or fill)):
