@@ -489,3 +489,14 @@ def test_large_recut_keeps_one_round_of_items():
     p = prepare(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q)
     assert p.abi.n_items[_native.TA_LARGE64] == 192
     assert _covers_paths_plan(p, schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), len(tree.paths))
+
+
+def test_fill_rule_leaves_long_private_parts_attached():
+    """The 64-row fill rule needs every small job to be one tile: the benchmark case `unequal`
+    (32 requests over a 1024-token root, private parts of 32..993 tokens) keeps its 128-row
+    root in 256-row items with private parts attached."""
+    from tree_attention import CostModel, schedule, shapes
+    tree = shapes.tree(shapes.benchmark_cases()["unequal"])
+    q = torch.zeros(len(tree.paths), 32, 128, dtype=torch.bfloat16)
+    p = prepare(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q)
+    assert p.abi.n_items[_native.TA_LARGE256] > 0 and p.abi.n_items[_native.TA_LARGE64] == 0 and p.attached
