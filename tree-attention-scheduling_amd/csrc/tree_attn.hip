@@ -432,7 +432,7 @@ __global__ __launch_bounds__(64 * NW) void seg_large_kernel(SegParams p) {
 }
 
 // ------------------------------------------------------------------ merge
-// One workgroup of MERGE_NT threads per (request, group of MH query heads);
+// One workgroup of NT threads per (request, group of MH query heads);
 // thread (head, d8) owns eight head-dim elements of one query head.  The slot
 // list is uniform per workgroup (scalar loads), and each thread reads, for
 // MERGE_CHUNK slots at once, the 16-byte partial slice (eight fp16 values) and
@@ -443,15 +443,20 @@ __global__ __launch_bounds__(64 * NW) void seg_large_kernel(SegParams p) {
 // the slots are computed and the partial loads are the first memory access.
 constexpr int MERGE_CHUNK = 16;
 constexpr int MERGE_NT = 128;
+// Below this many workgroups of MERGE_NT threads the merge runs groups of
+// MERGE_NT / 2 threads instead (half the heads per workgroup, twice the
+// workgroups): one workgroup per CU of the 256 leaves the GPU half empty, and
+// a small batch's merge is one round trip of loads per workgroup.
+constexpr int MERGE_FILL_BLOCKS = 256;
 
-// SPLIT groups of MERGE_NT threads split a request's slots into SPLIT
+// SPLIT groups of NT threads split a request's slots into SPLIT
 // contiguous ranges, merge them side by side (one round trip of loads per
 // MERGE_CHUNK slots each) and combine their running (max, sum, partial sums)
 // through LDS; the first group writes the output.  SPLIT = 2 serves plans with
 // more than MERGE_CHUNK slots per request: 32 slots wait for one round of loads
 // instead of two.  SPLIT = 1 is the single-group kernel described above.
-template <int D, bool FP16, int SPLIT>
-__global__ __launch_bounds__(MERGE_NT * SPLIT) void merge_kernel(const u16 *__restrict__ part,
+template <int D, bool FP16, int SPLIT, int NT = MERGE_NT>
+__global__ __launch_bounds__(NT * SPLIT) void merge_kernel(const u16 *__restrict__ part,
                                                                  const float *__restrict__ lse,
                                                                  const int32_t *__restrict__ slots,
                                                                  const int32_t *__restrict__ counts,
@@ -459,12 +464,12 @@ __global__ __launch_bounds__(MERGE_NT * SPLIT) void merge_kernel(const u16 *__re
                                                                  u16 *__restrict__ out, int hq, int maxs,
                                                                  int slot_stride) {
     constexpr int TPH = D / 8;          // threads per head
-    constexpr int MH = MERGE_NT / TPH;  // heads per workgroup
+    constexpr int MH = NT / TPH;  // heads per workgroup
     constexpr float LOG2E = 1.44269504088896341f;
     const int r = reqs ? reqs[blockIdx.x] : blockIdx.x;
     // a group is whole waves: readfirstlane tells the compiler grp is uniform
-    const int grp = SPLIT > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x / MERGE_NT) : 0;
-    const int tid = threadIdx.x % MERGE_NT;
+    const int grp = SPLIT > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x / NT) : 0;
+    const int tid = threadIdx.x % NT;
     const int hl = tid / TPH, d8 = tid % TPH;
     const int head = blockIdx.y * MH + hl;
     const bool valid = head < hq;
@@ -520,15 +525,15 @@ __global__ __launch_bounds__(MERGE_NT * SPLIT) void merge_kernel(const u16 *__re
         }
     }
     if constexpr (SPLIT > 1) {
-        __shared__ float sh[SPLIT - 1][10][MERGE_NT];
+        __shared__ float sh[SPLIT - 1][10][NT];
         if (grp > 0) {
             float *x = &sh[grp - 1][0][tid];
             x[0] = M;
-            x[MERGE_NT] = Z;
+            x[NT] = Z;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                x[(2 + i) * MERGE_NT] = lo[i];
-                x[(6 + i) * MERGE_NT] = hi[i];
+                x[(2 + i) * NT] = lo[i];
+                x[(6 + i) * NT] = hi[i];
             }
         }
         __syncthreads();
@@ -540,11 +545,11 @@ __global__ __launch_bounds__(MERGE_NT * SPLIT) void merge_kernel(const u16 *__re
             if (Mg == NEG_INF) continue;  // an empty range
             const float cm = fmaxf(M, Mg);
             const float alpha = fast_exp2(M - cm), beta = fast_exp2(Mg - cm);  // alpha is 0 while M is -inf
-            Z = Z * alpha + x[MERGE_NT] * beta;
+            Z = Z * alpha + x[NT] * beta;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                lo[i] = lo[i] * alpha + x[(2 + i) * MERGE_NT] * beta;
-                hi[i] = hi[i] * alpha + x[(6 + i) * MERGE_NT] * beta;
+                lo[i] = lo[i] * alpha + x[(2 + i) * NT] * beta;
+                hi[i] = hi[i] * alpha + x[(6 + i) * NT] * beta;
             }
             M = cm;
         }
@@ -622,15 +627,26 @@ template <int D, bool FP16>
 hipError_t launch_merge(const void *part, const float *lse, const int32_t *slots, const int32_t *counts,
                         const int32_t *reqs, void *out, int nreq, int hq, int maxs, hipStream_t stream,
                         int slot_stride = 0) {
-    constexpr int MH = MERGE_NT / (D / 8);
-    if (maxs > MERGE_CHUNK)
-        TA_LAUNCH((merge_kernel<D, FP16, 2>), dim3(nreq, (hq + MH - 1) / MH), dim3(2 * MERGE_NT), stream,
-                  static_cast<const u16 *>(part), lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs,
-                  slot_stride);
-    else
-        TA_LAUNCH((merge_kernel<D, FP16, 1>), dim3(nreq, (hq + MH - 1) / MH), dim3(MERGE_NT), stream,
-                  static_cast<const u16 *>(part), lse, slots, counts, reqs, static_cast<u16 *>(out), hq, maxs,
-                  slot_stride);
+    constexpr int MH = MERGE_NT / (D / 8), MH2 = MH / 2;
+    const bool fill = (long)nreq * ((hq + MH - 1) / MH) < MERGE_FILL_BLOCKS;
+    const dim3 grid(nreq, fill ? (hq + MH2 - 1) / MH2 : (hq + MH - 1) / MH);
+    const u16 *p16 = static_cast<const u16 *>(part);
+    u16 *o16 = static_cast<u16 *>(out);
+    if (maxs > MERGE_CHUNK) {
+        if (fill)
+            TA_LAUNCH((merge_kernel<D, FP16, 2, MERGE_NT / 2>), grid, dim3(MERGE_NT), stream, p16, lse, slots,
+                      counts, reqs, o16, hq, maxs, slot_stride);
+        else
+            TA_LAUNCH((merge_kernel<D, FP16, 2>), grid, dim3(2 * MERGE_NT), stream, p16, lse, slots, counts, reqs,
+                      o16, hq, maxs, slot_stride);
+    } else {
+        if (fill)
+            TA_LAUNCH((merge_kernel<D, FP16, 1, MERGE_NT / 2>), grid, dim3(MERGE_NT / 2), stream, p16, lse, slots,
+                      counts, reqs, o16, hq, maxs, slot_stride);
+        else
+            TA_LAUNCH((merge_kernel<D, FP16, 1>), grid, dim3(MERGE_NT), stream, p16, lse, slots, counts, reqs, o16,
+                      hq, maxs, slot_stride);
+    }
     return hipGetLastError();
 }
 
