@@ -77,6 +77,37 @@ def test_noalloc_equals_attention_matrix(device):
             assert abi.maxs > 16 and len(kinds) >= 2, (abi.maxs, kinds)
 
 
+def test_noalloc_on_register_staged_pools(device):
+    """Pools whose capacity is not a multiple of 8 run the register-staged kernels and the
+    unfused order (every kind writes partials, then all requests merge): the variant keeps
+    those partials in the array too.  Mixed kinds with up to 24 slots per request; two calls,
+    the second on a smaller layer, each bit-identical to ta_attention_matrix."""
+    for name, spec, seed in (("unequal, capacity 8k + 3", shapes.benchmark_cases()["unequal"], 31),
+                             ("deep, capacity 8k + 5", shapes.benchmark_cases()["deep"], 32)):
+        tree = shapes.tree(spec)
+        g = torch.Generator().manual_seed(seed)
+        t = -(-tree.storage_tokens // 8) * 8 + (3 if name.startswith("unequal") else 5)
+        q = torch.randn(len(tree.paths), 32, 128, generator=g).bfloat16().to(device)
+        k = torch.randn(t, 8, 128, generator=g).bfloat16().to(device)
+        v = torch.randn(t, 8, 128, generator=g).bfloat16().to(device)
+        kp, vp = pack_kv(k, v)
+        assert kp.shape[2] % 8 != 0
+        prepared = prepare(schedule(tree, 32, 8, 128, "cube", CostModel()), q).for_pools(kp)
+        abi = prepared.abi
+        assert not abi.xtail
+        say("noalloc register-staged", name, "slots", abi.nslot, "per request", abi.maxs, "items",
+            list(abi.n_items))
+        bare = _native.TaPlan.from_buffer_copy(abi)
+        bare.part, bare.lse = None, None
+        a = torch.empty_like(q)
+        b = torch.full_like(q, float("nan"))
+        assert _call("ta_attention_matrix", q, kp, vp, abi, a) == 0
+        assert _call("ta_attention_matrix_noalloc", q, kp, vp, bare, b) == 0
+        torch.cuda.synchronize()
+        assert torch.isfinite(b.float()).all(), name
+        assert torch.equal(a, b), name
+
+
 def test_noalloc_rejects_plans_beyond_its_array(device):
     q, kp, vp, prepared = _layer(shapes.benchmark_cases()["wide"], CostModel(), 3, device)
     big = _native.TaPlan.from_buffer_copy(prepared.abi)
