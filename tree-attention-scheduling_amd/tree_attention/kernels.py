@@ -569,10 +569,15 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     at most ``route_items`` (tile, KV head) units, the large jobs run as those
     groups in the small-job kernel instead (one segment launch less).
     ``large_target`` and ``small_target`` are the work items the re-cut aims at
-    for the large kinds and the small-job kind (default: one and eight per CU).
+    for the large kinds and the small-job kind (default: one and eight per CU);
+    a large re-cut that would leave a few items for a second round takes the
+    next longer chunks when one round of them is shorter.
     Large chunks of one tile are lengthened to ``large_min_tiles`` tiles when
     that keeps the kernel kinds and the attachments and gives at least half of
-    ``large_target`` work items.  Raises
+    ``large_target`` work items.  Jobs of at most ``consolidate_rows`` rows run
+    as 64-row request groups when 64-row items run anyway, or when their
+    256-row items would fill only a quarter to a half of the CUs and every
+    small job is one tile long (0: never).  Raises
     ``ValueError`` for jobs without requests or tokens, request ids outside
     ``q`` and token runs that are not consecutive physical ids.
     """
