@@ -500,3 +500,27 @@ def test_fill_rule_leaves_long_private_parts_attached():
     q = torch.zeros(len(tree.paths), 32, 128, dtype=torch.bfloat16)
     p = prepare(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()), q)
     assert p.abi.n_items[_native.TA_LARGE256] > 0 and p.abi.n_items[_native.TA_LARGE64] == 0 and p.attached
+
+
+def test_small_launch_takes_two_tile_chunks(monkeypatch):
+    """A launch of small-job items alone takes two-tile chunks when one-tile chunks would fill at
+    least 45 % of its 2048 waves: 32 requests over 1024-token contexts, 25 % shared, lower to
+    1664 two-tile items (8 partial slots per request) instead of 3328 one-tile items (16 slots),
+    and 16 such requests to 832 instead of 1664.  With 75 % shared, 16 requests give 896
+    one-tile items (44 % of the waves) and keep them."""
+    from tree_attention import CostModel, schedule, shapes
+    for nreq, fraction, one, two in ((32, 0.25, 3328, 1664), (16, 0.25, 1664, 832), (16, 0.75, 896, 896)):
+        tree = shapes.tree(shapes.grid_tree(nreq, 1024, fraction, 1))
+        q = torch.zeros(len(tree.paths), 32, 128, dtype=torch.bfloat16)
+        plan = schedule(tree, 32, 8, 128, "cube", CostModel.mi355x())
+        p = prepare(plan, q)
+        assert list(p.abi.n_items) == [two, 0, 0, 0, 0]
+        assert _covers_paths(p, tree)
+        monkeypatch.setattr(kernels, "SMALL_PAIRS", False)
+        assert list(prepare(plan, q).abi.n_items) == [one, 0, 0, 0, 0]
+        monkeypatch.setattr(kernels, "SMALL_PAIRS", True)
+    # two-tile chunks of 128 tokens: 2 of the shared 256 tokens and 6 of each private 768 per request
+    tree = shapes.tree(shapes.grid_tree(32, 1024, 0.25, 1))
+    p = prepare(schedule(tree, 32, 8, 128, "cube", CostModel.mi355x()),
+                torch.zeros(32, 32, 128, dtype=torch.bfloat16))
+    assert max(len(j.tokens) for j in p.jobs) == 128 and p.abi.maxs == 8

@@ -202,6 +202,13 @@ LARGE_MIN_TILES = 2
 # wider large jobs run as 64-row request groups when 64-row items run anyway and no wider
 # job exceeds this many rows (prepare's consolidate_rows; 0: never)
 CONSOLIDATE_ROWS = 128
+# a launch of small-job items alone (2048 one-wave workgroups, 8 per CU) takes two-tile chunks
+# instead of one-tile chunks when those would fill at least 45 % of its waves: a wave streams
+# the second tile of an item while it computes the first, and every chunk is one more partial
+# slot to merge.  Measured on the 81-shape grid, the reference's 81 trees and the calibration
+# trees (graph replay): 0.80-0.97x on most of the 70 layers it changes; with fuller thresholds
+# of 41-43 % of the waves two layers ran 1.11-1.15x.
+SMALL_PAIRS = True
 
 
 def _tiles(job) -> int:
@@ -346,7 +353,8 @@ def _fuse_same_tokens(jobs, group, min_rows):
     return out
 
 
-def _recut(jobs, items_per_chunk, target_items, is_fixed, min_tiles=1, floor_items=0, one_round=False):
+def _recut(jobs, items_per_chunk, target_items, is_fixed, min_tiles=1, floor_items=0, one_round=False,
+           pairs=False):
     """Execution jobs for one kernel kind: runs of consecutive jobs over the same
     requests and contiguous tokens are cut again into near-equal chunks, as long
     as possible while the kind still gets ``target_items`` work items (one
@@ -359,6 +367,8 @@ def _recut(jobs, items_per_chunk, target_items, is_fixed, min_tiles=1, floor_ite
     gives a few more than that runs a second round of items for them; the next
     longer cut, one round of longer chunks, is taken when its chunks are shorter
     than the rounds' chunks end to end.
+    ``pairs``: chunks are two tiles long, not one, when one-tile chunks would give at
+    least 45 % of ``target_items`` items.
     """
     runs = []  # [requests, first token, length, fixed]
     for job in jobs:
@@ -396,6 +406,8 @@ def _recut(jobs, items_per_chunk, target_items, is_fixed, min_tiles=1, floor_ite
         rounds = -(-count(lo * TOKEN_QUANTUM) // target_items)
         if rounds > 1 and hi < rounds * lo:  # count(hi) < target_items: one round
             lo = hi
+    if pairs and lo == 1 and hi == 2 and 20 * count(TOKEN_QUANTUM) >= 9 * target_items:
+        lo = 2
     if lo < min_tiles and count(min_tiles * TOKEN_QUANTUM) >= floor_items:
         lo = min_tiles
     limit = lo * TOKEN_QUANTUM
@@ -696,7 +708,8 @@ def prepare(plan: Plan, q: torch.Tensor, tile_rows: int = 256, fixed_from: int |
     longest = max((_tiles(j) for j in tails), default=0)
     enough = len(tails) * kvheads >= n_cu * (1 if longest <= TAIL_KEEP_TILES else TAIL_KEEP_ITEMS_PER_CU)
     keep = {id(j) for j in tails} if enough else set()
-    small = _recut(small, lambda r: kvheads, small_target, lambda j: growing(j) or id(j) in keep)
+    small = _recut(small, lambda r: kvheads, small_target, lambda j: growing(j) or id(j) in keep,
+                   pairs=SMALL_PAIRS and not large)
     jobs = small + large
     small_jobs = len(small)
     njobs = len(jobs)
