@@ -146,6 +146,27 @@ def test_nested_unequal_tree(device):
             check(out, ref, 0.008, 0.03, f"nested/{method}")
 
 
+def test_small_launch_two_tile_chunks(device, monkeypatch):
+    """A launch of small-job items alone with two-tile chunks (prepare's SMALL_PAIRS: 32
+    requests over 1024-token contexts, 25 % shared, lower to 1664 two-tile items, 8 slots per
+    request) matches the oracle, as the same plan lowered to 3328 one-tile items does."""
+    from tree_attention import kernels
+    tree = shapes.tree(shapes.grid_tree(32, 1024, 0.25, 1))
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 43)
+    plan = schedule(tree, 32, 8, 128, "cube", CostModel.mi355x())
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    ref = oracle_fp32(q, k, v, tree)
+    for pairs, items, slots in ((True, 1664, 8), (False, 3328, 16)):
+        monkeypatch.setattr(kernels, "SMALL_PAIRS", pairs)
+        prepared = prepare(plan, qd)
+        assert list(prepared.abi.n_items) == [items, 0, 0, 0, 0] and prepared.abi.maxs == slots
+        say("two-tile chunks", pairs, "items", items)
+        out = attention_matrix(qd, kp, vp, prepared)
+        torch.cuda.synchronize()
+        check(out, ref, 0.008, 0.03, f"small launch, pairs={pairs}")
+
+
 @pytest.mark.parametrize("hq,hk,d", [(8, 2, 32), (8, 2, 64), (32, 8, 128)])
 def test_merge_of_many_slots(hq, hk, d, device):
     """More than 16 partial slots per request (the merge splits them into two ranges), ragged counts
