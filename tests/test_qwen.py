@@ -276,6 +276,44 @@ def test_fused_decode_glue_equals_eager_glue(dtype, device):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_graph_decode_equals_eager_decode(dtype, device):
+    """CachedPrefixDecoder(graph=True) captures the first step's forward in a HIP graph and
+    replays it: every step's logits and the pools equal the eager decoder's, bit for bit,
+    with the host's own work between the replays; the step past max_new_tokens is refused
+    and leaves the decoder as it was."""
+    model = tiny_model(dtype, device)
+    graphed = integration.CachedPrefixDecoder(model, SEQUENCES, 4, "cube", graph=True)
+    eager = integration.CachedPrefixDecoder(model, SEQUENCES, 4, "cube")
+    kept = []
+    for _ in range(4):
+        tokens = eager.logits.argmax(-1).tolist()
+        a, b = graphed.step(tokens), eager.step(tokens)
+        kept.append(a)
+        assert torch.equal(a, b)
+        torch.cuda.synchronize()
+    assert graphed._replay is not None
+    # returned logits are the caller's: later replays do not overwrite them
+    assert not any(kept[i].data_ptr() == kept[j].data_ptr() for i in range(4) for j in range(i))
+    written = list(range(graphed.prefix_size)) + [graphed.prefix_size + r * graphed.max_new_tokens + t
+                                                  for r in range(len(SEQUENCES)) for t in range(graphed.generated)]
+    idx = torch.tensor(written, device=device)
+    for (kp1, vp1), (kp2, vp2) in zip(graphed.pools, eager.pools):
+        assert torch.equal(kp1.index_select(2, idx), kp2.index_select(2, idx))
+        assert torch.equal(vp1.index_select(1, idx), vp2.index_select(1, idx))
+    before = (graphed.generated, [list(s) for s in graphed.sequences])
+    with pytest.raises(ValueError):
+        graphed.step(eager.logits.argmax(-1).tolist())
+    assert (graphed.generated, graphed.sequences) == before
+
+
+def test_graph_decode_needs_the_gpu_cpu():
+    model = tiny_model(torch.float32, torch.device("cpu"))
+    with pytest.raises(ValueError):
+        integration.CachedPrefixDecoder(model, SEQUENCES, 2, "cube", graph=True)
+
+
+@pytest.mark.gpu
 def test_per_layer_attention_vs_oracle_gpu(device, monkeypatch):
     """scripts/model_checks.py:42-64: every layer's tree attention vs FP32 on the same Q/K/V."""
     model = tiny_model(torch.bfloat16, device)

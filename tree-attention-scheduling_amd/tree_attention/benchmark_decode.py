@@ -100,8 +100,8 @@ def main(argv=None):
                    "argmax_agree": round((l.argmax(-1) == truth.argmax(-1)).float().mean().item(), 4)}
                for m, l in prefill_logits.items()}
     decoders = {name: integration.CachedPrefixDecoder(model, sequences, budget, args.method, CostModel.mi355x(),
-                                                      fused_glue=fused, prefill=args.prefill)
-                for name, fused in (("fused", True), ("eager", False))}
+                                                      fused_glue=fused, prefill=args.prefill, graph=graph)
+                for name, fused, graph in (("fused", True, False), ("eager", False, False), ("graph", True, True))}
     torch.cuda.synchronize()
 
     original = integration.attention_matrix
@@ -133,8 +133,8 @@ def main(argv=None):
                 "median": round(statistics.median(rel), 6), "per_layer": [round(x, 6) for x in rel]}
 
     step_ms = {name: [] for name in decoders}
-    attn_us = {name: [] for name in decoders}
-    identical = True
+    attn_us = {name: [] for name in decoders if name != "graph"}
+    identical = graph_identical = True
     recording = False
     layer_rel_l2 = {}
     integration.attention_matrix = timed_attention
@@ -145,6 +145,8 @@ def main(argv=None):
             for name, decoder in decoders.items():
                 recording = name == "fused" and step in check_steps
                 attn_events.clear()
+                # the graph decoder captures the plain call (no events inside a capture)
+                integration.attention_matrix = original if name == "graph" else timed_attention
                 torch.cuda.synchronize()
                 t0 = time.perf_counter()
                 logits[name] = decoder.step(tokens)
@@ -155,8 +157,10 @@ def main(argv=None):
                     layer_rel_l2[step] = layer_errors(decoder, step)
                 elif step >= args.warmup and step not in check_steps:
                     step_ms[name].append(dt)
-                    attn_us[name].append(statistics.mean(a.elapsed_time(b) * 1e3 for a, b in attn_events))
+                    if name in attn_us:
+                        attn_us[name].append(statistics.mean(a.elapsed_time(b) * 1e3 for a, b in attn_events))
             identical &= bool(torch.equal(logits["fused"], logits["eager"]))
+            graph_identical &= bool(torch.equal(logits["fused"], logits["graph"]))
     finally:
         integration.attention_matrix = original
 
@@ -172,6 +176,8 @@ def main(argv=None):
         "glue_saving_us_per_layer": round((statistics.median(step_ms["eager"]) - statistics.median(step_ms["fused"]))
                                           * 1e3 / args.layers, 2),
         "fused_equals_eager": identical,
+        "graph_equals_fused": graph_identical,
+        "graph_speedup": round(statistics.median(step_ms["fused"]) / statistics.median(step_ms["graph"]), 2),
         "timed_steps": len(step_ms["fused"]),
         "attention_rel_l2_vs_fp32": {str(k): v for k, v in sorted(layer_rel_l2.items())},
         "plan": {"jobs": len(cached.jobs), "items": list(cached.abi.n_items), "attached": len(cached.attached)},

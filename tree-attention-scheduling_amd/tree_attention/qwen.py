@@ -242,8 +242,16 @@ class SharedKVDecoder:
         positions = self._append(token_ids)
         slots = torch.tensor(positions, device=self.device, dtype=torch.int32)
         prepared = self._prepare_plan()
+        ids = torch.tensor(token_ids, device=self.device)[:, None]
+        self.logits = self._forward(ids, rope_pos, slots, prepared)
+        return self.logits
+
+    def _forward(self, ids, rope_pos, slots, prepared, **model_kwargs):
+        """The model's forward over one token per request, each layer's attention swapped for one
+        that writes the step's RoPE'd K/V into pool ``slots`` and attends the pools with
+        ``prepared``; returns the logits ``[R, vocab]``."""
         pools = self.pools
-        nreq = len(token_ids)
+        nreq = ids.shape[0]
         fused = self.fused_glue
 
         def forward(module, hidden_states, position_embeddings, attention_mask=None, **kwargs):
@@ -269,25 +277,71 @@ class SharedKVDecoder:
         for layer in layers:
             layer.self_attn.forward = MethodType(forward, layer.self_attn)
         try:
-            out = self.model(torch.tensor(token_ids, device=self.device)[:, None], position_ids=rope_pos,
-                             use_cache=False)
-            self.logits = out.logits[:, 0]
+            out = self.model(ids, position_ids=rope_pos, use_cache=False, **model_kwargs)
+            return out.logits[:, 0]
         finally:
             for layer, original in zip(layers, self.original):
                 layer.self_attn.forward = original
-        return self.logits
 
 
 class CachedPrefixDecoder(SharedKVDecoder):
-    """Plans the prompt tree once; each step only sets the decode-tail lengths (qwen.py:106-124)."""
+    """Plans the prompt tree once; each step only sets the decode-tail lengths (qwen.py:106-124).
+
+    ``graph=True`` (a bf16 / fp16 model on the GPU) runs the first step's forward eagerly, then
+    captures it in a HIP graph over fixed input buffers (token ids, RoPE positions, pool slots)
+    and the plan's fixed metadata; every later step writes its inputs into those buffers, sets
+    the tails' lengths on the device and replays the graph.  The logits are bit-identical to
+    the eager steps'; the host no longer launches each of the model's kernels.  The argument
+    has no counterpart in the reference.
+    """
 
     def __init__(self, model, sequences, max_new_tokens=32, method="cube", cost_model=None, fused_glue=None,
-                 prefill="request"):
+                 prefill="request", graph=False):
         super().__init__(model, sequences, max_new_tokens, method, cost_model, fused_glue, prefill)
+        if graph and not (self.device.type == "cuda" and self.fused_glue):
+            raise ValueError("graph=True needs a bfloat16 or float16 model on the GPU (the fused decode glue)")
         prompt_plan = schedule(self.tree, self.hq, self.hk, self.dim, self.method, self.cost_model)
         shape_of_q = torch.empty((len(self.sequences), self.hq, self.dim), device=self.device,
                                  dtype=model.dtype)
         self.cached_plan = CachedDecodePlan(prompt_plan, shape_of_q, self.prefix_size, max_new_tokens)
+        self.graph = graph
+        self._replay = None  # (graph, ids, positions, slots, logits) once captured
+
+    @torch.inference_mode()
+    def step(self, token_ids):
+        if not self.graph:
+            return super().step(token_ids)
+        token_ids = list(token_ids)
+        nreq = len(self.sequences)
+        if len(token_ids) != nreq:
+            raise ValueError("step needs exactly one token per request")
+        self._check_append(nreq)
+        cap = self.pools[0][0].shape[2]
+        planned = self._step_slots(nreq)
+        if not all(0 <= p < cap for p in planned):
+            raise ValueError(f"pool slots {planned} outside the pool capacity {cap}")
+        ids = torch.tensor(token_ids, device=self.device)[:, None]
+        rope_pos = torch.tensor([[len(s)] for s in self.sequences], device=self.device)
+        slots = torch.tensor(planned, device=self.device, dtype=torch.int32)
+        self._append(token_ids)
+        prepared = self._prepare_plan()  # the tails' lengths, set on the device in stream order
+        # the masks of every layer type, none built: the swapped attention takes none
+        no_mask = {t: None for t in set(self.model.config.layer_types)}
+        if self._replay is None:
+            logits = self._forward(ids, rope_pos, slots, prepared, attention_mask=no_mask)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                out = self._forward(ids, rope_pos, slots, prepared, attention_mask=no_mask)
+            self._replay = (graph, ids, rope_pos, slots, out)
+        else:
+            graph, ids_buf, pos_buf, slots_buf, out = self._replay
+            ids_buf.copy_(ids)
+            pos_buf.copy_(rope_pos)
+            slots_buf.copy_(slots)
+            graph.replay()
+            logits = out
+        self.logits = logits.clone()
+        return self.logits
 
     def _check_append(self, count):
         if self.generated >= self.max_new_tokens:
