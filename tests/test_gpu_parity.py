@@ -445,8 +445,12 @@ def test_tail_items_with_merge_rest(dtype, device):
     check(out, oracle_fp32(q, k, v, tree), 0.006, 0.02, "tail+rest")
 
 
-def test_cached_decode_plan_steps(device):
-    """scripts/benchmark_decode_plan.py protocol: 32 req, 1024 + 64 prompt, growing tails, check steps."""
+@pytest.mark.parametrize("model_name", ["reference", "mi355x"])
+def test_cached_decode_plan_steps(model_name, device):
+    """scripts/benchmark_decode_plan.py protocol: 32 req, 1024 + 64 prompt, growing tails, check steps,
+    planned under the reference's cost model and the fitted one (whose 32-request root runs as
+    64-row request groups beside the tails' small items, prepare's fill rule)."""
+    model = CostModel() if model_name == "reference" else CostModel.mi355x()
     base = shapes.tree(shapes.shared_prefix(32, 1024, 64))
     prefix = base.storage_tokens
     steps = 16
@@ -457,9 +461,11 @@ def test_cached_decode_plan_steps(device):
     qd = q.to(device)
     kp, vp = pack_kv(k.to(device), v.to(device))
     for method in ("fixed", "cube"):
-        cached = CachedDecodePlan(schedule(base, method=method), qd, prefix, steps)
+        cached = CachedDecodePlan(schedule(base, method=method, model=model), qd, prefix, steps)
+        if method == "cube":
+            assert cached.prepared.abi.n_items[_native.TA_LARGE64] > 0 and not cached.prepared.attached
         for step in (0, 7, steps - 1):
-            say("decode", method, step)
+            say("decode", model_name, method, step)
             out = attention_matrix(qd, kp, vp, cached.update(step + 1)).cpu()
             paths = [p + tuple(prefix + r * steps + t for t in range(step + 1)) for r, p in enumerate(base.paths)]
             ref = oracle_fp32(q, k, v, KVTree([], paths))
@@ -467,6 +473,22 @@ def test_cached_decode_plan_steps(device):
         # zero generated tokens: tails contribute nothing (reference leaves this undefined)
         out = attention_matrix(qd, kp, vp, cached.update(0)).cpu()
         check(out, oracle_fp32(q, k, v, base), 0.008, 0.03, f"decode/{method}/empty-tail")
+
+
+def test_large_items_in_one_round(device):
+    """32 requests over a 4096-token context, 99 % shared in three levels: the large re-cut takes
+    one round of longer chunks (192 64-row items instead of 272) under the fitted model; the
+    layer matches the oracle, as the same plan with the shorter cut does."""
+    tree = shapes.tree(shapes.grid_tree(32, 4096, 0.99, 3))
+    q, k, v = make_inputs(tree, 32, 8, 128, torch.bfloat16, 47)
+    qd = q.to(device)
+    kp, vp = pack_kv(k.to(device), v.to(device))
+    plan = schedule(tree, 32, 8, 128, "cube", CostModel.mi355x())
+    prepared = prepare(plan, qd)
+    assert prepared.abi.n_items[_native.TA_LARGE64] == 192
+    out = attention_matrix(qd, kp, vp, prepared)
+    torch.cuda.synchronize()
+    check(out, oracle_fp32(q, k, v, tree), 0.008, 0.03, "one round")
 
 
 @pytest.mark.parametrize("model_name", ["mi355x", "mi355x-like"])
