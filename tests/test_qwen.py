@@ -276,15 +276,16 @@ def test_fused_decode_glue_equals_eager_glue(dtype, device):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_graph_decode_equals_eager_decode(dtype, device):
+@pytest.mark.parametrize("dtype,method,prefill", [(torch.float16, "cube", "request"), (torch.bfloat16, "cube", "tree"),
+                                                  (torch.bfloat16, "fixed", "request")])
+def test_graph_decode_equals_eager_decode(dtype, method, prefill, device):
     """CachedPrefixDecoder(graph=True) captures the first step's forward in a HIP graph and
     replays it: every step's logits and the pools equal the eager decoder's, bit for bit,
     with the host's own work between the replays; the step past max_new_tokens is refused
     and leaves the decoder as it was."""
     model = tiny_model(dtype, device)
-    graphed = integration.CachedPrefixDecoder(model, SEQUENCES, 4, "cube", graph=True)
-    eager = integration.CachedPrefixDecoder(model, SEQUENCES, 4, "cube")
+    graphed = integration.CachedPrefixDecoder(model, SEQUENCES, 4, method, graph=True, prefill=prefill)
+    eager = integration.CachedPrefixDecoder(model, SEQUENCES, 4, method, prefill=prefill)
     kept = []
     for _ in range(4):
         tokens = eager.logits.argmax(-1).tolist()
